@@ -1,0 +1,282 @@
+"""op1 benchmark on one MI355X: Mixtral-8x7B MoE layer over a 64-node tree.
+
+One step = one ``tree_moe_forward`` call (router, budget routing/bucketing,
+gate/up GEMM + SwiGLU, down GEMM, fixed-order combine) at config 2 of the
+baseline: T=64, H=4096, I=14336, E=8, top-2, B=8, bf16, inputs resident in
+HBM.  ``value`` is algorithmic HBM throughput (compulsory bytes / step time).
+
+Prints ONE JSON line.  Also reports, in the same line, the dominant kernel's
+roofline (HIP events on the launch stream), the CPU baseline (torch
+restatement of treemoe/ref on the host cores), and secondary configurations.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+METRIC = "op1 MoE layer µs + HBM GB/s (% peak), Mixtral shape, 64-node tree, 1 MI355X"
+
+
+def parse_args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--cpu-seconds", type=float, default=15.0,
+                   help="time budget of the CPU-baseline sample (0 disables it)")
+    p.add_argument("--no-secondary", action="store_true")
+    return p.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def events_time_ms(fn, reps: int) -> float:
+    """Mean wall time of fn() on the current stream, HIP events."""
+    import torch
+
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def kernel_breakdown(m, inp, reps: int) -> dict:
+    """Average duration (ms) of each launch of one op1 step, events placed on
+    the stream the library launches on (torch's current stream)."""
+    import torch
+
+    from treemoe_spec_amd import _capi
+
+    x, w1, w2, w3, router, accept, budget = (inp.x, inp.w1, inp.w2, inp.w3, inp.router,
+                                             inp.accept, inp.budget)
+    n, hidden = x.shape
+    e, inter, _ = w1.shape
+    stream = _capi.stream_of(x.device)
+    names = ["route", "gemm1", "gemm2", "combine"]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(reps)]
+    out = torch.empty_like(x)
+    for r in range(reps):
+        ev[r][0].record()
+        routing = m.route_experts(x, router, accept, budget, inter)
+        ws = routing.ws
+        ev[r][1].record()
+        _capi.call("tm_op1_gemm1", x.data_ptr(), w1.data_ptr(), w3.data_ptr(), ws.h.data_ptr(),
+                   routing.sorted_slots.data_ptr(), routing.tiles.data_ptr(),
+                   routing.max_tiles, n, hidden, inter, e, stream)
+        ev[r][2].record()
+        _capi.call("tm_op1_gemm2", ws.h.data_ptr(), w2.data_ptr(), ws.partial.data_ptr(),
+                   routing.gates_flat.data_ptr(), routing.sorted_slots.data_ptr(),
+                   routing.tiles.data_ptr(), routing.max_tiles, ws.split, n, hidden, inter, e,
+                   stream)
+        ev[r][3].record()
+        _capi.call("tm_op1_combine", ws.partial.data_ptr(), routing.slot_pos.data_ptr(),
+                   out.data_ptr(), n, hidden, ws.split, stream)
+        ev[r][4].record()
+    torch.cuda.synchronize()
+    res = {}
+    for k, name in enumerate(names):
+        res[name] = sum(ev[r][k].elapsed_time(ev[r][k + 1]) for r in range(reps)) / reps
+    return res
+
+
+def measured_traffic(profile: Path) -> float | None:
+    """HBM bytes per gemm1 launch from the committed rocprofv3 --pmc summary
+    (line 'gemm1_hbm_bytes_per_launch: <bytes>'), None if absent."""
+    if not profile.exists():
+        return None
+    for line in profile.read_text().splitlines():
+        if line.startswith("gemm1_hbm_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
+def cpu_baseline(inp, budget_s: float, bytes_alg: int) -> dict:
+    import torch
+
+    from oracle import op1_ref
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    cpu = [t.detach().cpu() for t in (inp.x, inp.w1, inp.w2, inp.w3, inp.router, inp.accept)]
+    op1_ref.tree_moe_forward(*cpu, inp.budget)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        op1_ref.tree_moe_forward(*cpu, inp.budget)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 200:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": round(bytes_alg / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} full config-2 layers (T=64, H=4096, I=14336, E=8, B=8) "
+                   f"through the torch CPU restatement of treemoe/ref/tree_moe_ref.py; "
+                   f"median {med * 1e3:.1f} ms/layer; host {platform.processor() or platform.machine()}, "
+                   f"os.cpu_count()={threads}"),
+        "ms_per_layer": round(med * 1e3, 3),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the op1/op4 path is built and measured on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+    from treemoe_spec_amd.workloads import (op1_algorithmic_bytes, op1_flops, op1_workload)
+
+    torch.cuda.set_device(0)
+    log("drawing config 2 inputs")
+    inp = op1_workload("config2_mixtral_t64_b8", device="cuda")
+    t, h, i, e = inp.shape
+    fwd = lambda: m.tree_moe_forward(inp.x, inp.w1, inp.w2, inp.w3, inp.router, inp.accept,
+                                     inp.budget)
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    routing = m.route_experts(inp.x, inp.router, inp.accept, inp.budget, i)
+    n_active = len(routing.expert_ids())
+    bytes_alg = op1_algorithmic_bytes(t, h, i, e, n_active)
+    flops = op1_flops(t, h, i, e)
+
+    log(f"timing {args.steps} steps")
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    ms = events_time_ms(fwd, args.steps)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - w0) * 1e3 / args.steps
+
+    bd = kernel_breakdown(m, inp, args.steps)
+    gemm1_bytes = e_act_bytes = n_active * 2 * h * i * 2  # w1 + w3 of active experts
+    gemm1_bytes += t * h * 2  # x
+    gemm1_gbs = gemm1_bytes / (bd["gemm1"] * 1e-3) / 1e9
+    gemm2_bytes = n_active * h * i * 2
+    gemm2_gbs = gemm2_bytes / (bd["gemm2"] * 1e-3) / 1e9
+    del e_act_bytes
+    traffic = measured_traffic(ROOT / "profiles" / "op1_gemm1_config2_pmc.txt")
+    value = bytes_alg / (ms * 1e-3) / 1e9
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "us_per_layer": round(ms * 1e3, 2),
+        "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "op1 Mixtral-8x7B MoE layer, T=64 tree tokens, top-2, B=8 (config 2)",
+                   "tokens": t, "hidden": h, "ffn": i, "experts": e, "budget": inp.budget,
+                   "active_experts": n_active, "bytes_alg": bytes_alg, "flops_alg": flops},
+        "roofline": {"bound": "hbm", "kernel": "tm_gemm1_kernel",
+                     "achieved": round(gemm1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gemm1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_alg_per_launch": gemm1_bytes,
+                     "avg_launch_us": round(bd["gemm1"] * 1e3, 2)},
+        "kernels_us": {k: round(v * 1e3, 2) for k, v in bd.items()},
+        "gemm2_gbs": round(gemm2_gbs, 1),
+        "wall_ms_per_step": round(wall_ms, 4),
+        "tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+    }
+
+    if not args.no_secondary:
+        line["secondary"] = secondary(m, inp, args)
+    if args.cpu_seconds > 0:
+        log("CPU baseline")
+        line["cpu_baseline"] = cpu_baseline(inp, args.cpu_seconds, bytes_alg)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+def secondary(m, inp2, args) -> dict:
+    """Config 3 (B=4 skew), config 5 (T=2048 Zipf) and op4 (config 4), reusing
+    config 2's expert weights (weights do not affect timing; routing inputs
+    follow each config's own seed)."""
+    import torch
+
+    from treemoe_spec_amd.kernels import op4_commit
+    from treemoe_spec_amd.kv_cache import MixtralConfig, PagedKVCache
+    from treemoe_spec_amd.workloads import (op1_algorithmic_bytes, op1_flops, op1_workload,
+                                            op4_algorithmic_bytes, op4_workload)
+
+    out = {}
+    weights = (inp2.w1, inp2.w2, inp2.w3)
+    reps = max(10, args.steps // 2)
+    for name in ("config3_mixtral_t64_b4_skew", "config5_mixtral_t2048_zipf"):
+        log(f"secondary {name}")
+        inp = op1_workload(name, device="cuda", weights=weights)
+        t, h, i, e = inp.shape
+        fwd = lambda: m.tree_moe_forward(inp.x, inp.w1, inp.w2, inp.w3, inp.router,
+                                         inp.accept, inp.budget)
+        for _ in range(3):
+            fwd()
+        ms = events_time_ms(fwd, reps)
+        r = m.route_experts(inp.x, inp.router, inp.accept, inp.budget, i)
+        n_active = len(r.expert_ids())
+        b = op1_algorithmic_bytes(t, h, i, e, n_active)
+        fl = op1_flops(t, h, i, e)
+        out[name] = {"us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                     "pct_hbm_peak": round(100 * b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                     "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
+                     "pct_mfma_peak": round(100 * fl / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 2),
+                     "active_experts": n_active}
+    log("secondary op4 config 4")
+    w = op4_workload(n=64, vocab=32000, max_depth=8, seed=3)
+    cfg = MixtralConfig()
+    page = 16
+    kv = PagedKVCache(cfg, 4096 // page + 4 + 16, device="cuda", page_size=page, tree_size=64)
+    kv._ensure_capacity(4096)
+    logits = w.logits.cuda()
+    tokens = w.tokens.cuda()
+    parent = w.parent.cuda()
+
+    def step():
+        kv.seq_len = 4096
+        return op4_commit.fused_verify_commit(logits, None, tokens, parent, w.children, kv=kv,
+                                              max_depth=8)
+
+    for _ in range(3):
+        res = step()
+    num = int(res.num_accepted)
+    ms = events_time_ms(step, reps)
+    b = op4_algorithmic_bytes(64, 32000, 2, num + 1, cfg.num_layers,
+                              cfg.num_kv_heads * cfg.head_dim * 2)
+    out["config4_op4_verify_commit"] = {"us_incl_host_sync": round(ms * 1e3, 2),
+                                        "accepted": num, "bytes_alg": b}
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,181 @@
+/*
+ * treemoe_amd.h — C ABI of the MI355X (gfx950) verification hot path.
+ *
+ * One shared library, libtreemoe_amd.so, exports the entry points below.  They
+ * replace the GPU work behind the reference's Python operators:
+ *
+ *   op1  tree_moe_forward / route_experts   treemoe/kernels/op1_tree_moe.py:641-802
+ *   op4  fused_verify_commit                treemoe/kernels/op4_commit.py:170-272
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers and sizes; no torch types, no allocation inside;
+ *   - every call is asynchronous on `stream` (a hipStream_t, may be NULL for the
+ *     null stream) and is the last argument;
+ *   - the return value is 0 (TM_OK) on success, a TM_ERR_* argument code when a
+ *     size/shape check fails before any launch, or a hipError_t value (offset by
+ *     TM_ERR_HIP_BASE) when a launch fails;
+ *   - bf16 tensors are passed as raw 16-bit storage (`const void*`), row-major
+ *     and contiguous unless a stride argument says otherwise;
+ *   - calls that share workspace buffers must be serialised on one stream.
+ */
+#ifndef TREEMOE_AMD_H
+#define TREEMOE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TM_OK 0
+#define TM_ERR_SHAPE 1001      /* a size argument is out of the supported range */
+#define TM_ERR_ALIGN 1002      /* a pointer or stride is not suitably aligned   */
+#define TM_ERR_ARG 1003        /* an enumerated argument has an unknown value   */
+#define TM_ERR_HIP_BASE 2000   /* TM_ERR_HIP_BASE + hipError_t                  */
+
+#define TM_OBJECTIVE_MASS 0
+#define TM_OBJECTIVE_CRITICAL_PATH 1
+
+#define TM_DTYPE_F32 0
+#define TM_DTYPE_BF16 1
+
+/* Limits checked by the entry points. */
+#define TM_MAX_EXPERTS 64
+#define TM_MAX_TOKENS 4096
+#define TM_GEMM_TILE_M 64      /* rows of one expert processed per GEMM tile */
+
+/* ABI version (major*10000 + minor*100 + patch). */
+int tm_version(void);
+
+/* Human-readable text for a return code of any entry point. */
+const char* tm_status_string(int code);
+
+/* ---------------------------------------------------------------- op1 -- */
+
+/*
+ * Router: gates[t, e] = softmax_e( bf16( x[t, :] . wg[e, :] ) ), fp32.
+ * Replaces `F.linear(x, W_g)` + `torch.softmax(logits.float(), -1)` at
+ * treemoe/kernels/op1_tree_moe.py:676-677 (same maths as
+ * treemoe/ref/tree_moe_ref.py:83-84).  x: [T, H] bf16, wg: [E, H] bf16,
+ * gates: [T, E] fp32.  Requires H % 8 == 0, 1 <= T <= TM_MAX_TOKENS,
+ * 2 <= E <= TM_MAX_EXPERTS.
+ */
+int tm_op1_router_gates(const void* x, const void* wg, int64_t T, int64_t H,
+                        int64_t E, float* gates, void* stream);
+
+/*
+ * Budget routing + stable (expert, DFS) bucketing in one workgroup.
+ * Replaces `_budget_bucket_fused_kernel` (treemoe/kernels/op1_tree_moe.py:159-297)
+ * and its torch fallback `route_and_bucket` (:81-149); semantics of
+ * `budget_route_ref` (treemoe/ref/tree_moe_ref.py:14-67) and
+ * `route_and_bucket_ref` (:70-99).
+ *
+ * Inputs : gates [T, E] fp32, accept [T] fp32, budget in [2, E], tau,
+ *          objective (TM_OBJECTIVE_*), block_m (16 or 32) and max_blocks
+ *          (= compact_block_capacity(2T, budget, block_m)) for the reference's
+ *          padded layout, max_tiles (= compact_block_limit(2T, budget,
+ *          TM_GEMM_TILE_M)) for the GEMM tile list.
+ * Outputs (reference layout, all written every call):
+ *          topk_ids [2T] i64, gates_flat [2T] f32, padded_slots
+ *          [max_blocks*block_m] i64 (-1 pad), block_expert_ids [max_blocks] i64
+ *          (-1 unused), slot_to_row [2T] i64, demand [E] f32;
+ * Outputs (compact layout used by the GEMMs):
+ *          expert_offsets [E+1] i32, sorted_slots [2T] i32 (expert-major,
+ *          DFS-stable), slot_pos [2T] i32 (inverse of sorted_slots),
+ *          tiles [max_tiles*4] i32 = (expert or -1, first sorted row, rows, 0).
+ */
+int tm_op1_route_bucket(const float* gates, const float* accept, int64_t T,
+                        int64_t E, int64_t budget, float tau, int objective,
+                        int64_t block_m, int64_t max_blocks, int64_t max_tiles,
+                        int64_t* topk_ids, float* gates_flat,
+                        int64_t* padded_slots, int64_t* block_expert_ids,
+                        int64_t* slot_to_row, float* demand,
+                        int32_t* expert_offsets, int32_t* sorted_slots,
+                        int32_t* slot_pos, int32_t* tiles, void* stream);
+
+/*
+ * Gate/up projection + SwiGLU for every routed slot.
+ * Replaces `_moe_gemm1_kernel` (treemoe/kernels/op1_tree_moe.py:300-383):
+ *   h[p, :] = bf16( silu(x[tok] . w1[e]^T) * (x[tok] . w3[e]^T) ), fp32 accumulate,
+ * for sorted row p of expert e, tok = sorted_slots[p] / 2.
+ * x: [T, H] bf16, w1/w3: [E, I, H] bf16, h: [2T, I] bf16 (workspace).
+ * Requires H % 256 == 0 and I % 64 == 0.
+ */
+int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void* h,
+                 const int32_t* sorted_slots, const int32_t* tiles,
+                 int64_t max_tiles, int64_t T, int64_t H, int64_t I, int64_t E,
+                 void* stream);
+
+/*
+ * Down projection, split over K = I into `split` deterministic segments.
+ * Replaces `_moe_gemm2_det_kernel` (treemoe/kernels/op1_tree_moe.py:447-509):
+ *   y[s, p, :] = gates_flat[slot] * ( h[p, Ks] . w2[e][:, Ks]^T ), fp32,
+ * h: [2T, I] bf16, w2: [E, H, I] bf16, y: [split, 2T, H] fp32 (workspace).
+ * Requires H % 64 == 0 and (I / split) % 256 == 0.
+ */
+int tm_op1_gemm2(const void* h, const void* w2, float* y,
+                 const float* gates_flat, const int32_t* sorted_slots,
+                 const int32_t* tiles, int64_t max_tiles, int64_t split,
+                 int64_t T, int64_t H, int64_t I, int64_t E, void* stream);
+
+/*
+ * Fixed-order combine.  Replaces `_combine_kernel`
+ * (treemoe/kernels/op1_tree_moe.py:512-529) and the final `.to(x.dtype)` (:798):
+ *   out[t, :] = bf16( ((y[0,p0] + .. + y[S-1,p0]) + y[0,p1]) + .. + y[S-1,p1] )
+ * with p_k = slot_pos[2t + k].  out: [T, H] bf16.  Requires H % 4 == 0.
+ */
+int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
+                   int64_t T, int64_t H, int64_t split, void* stream);
+
+/* ---------------------------------------------------------------- op4 -- */
+
+/*
+ * First-occurrence argmax per tree node + greedy accept walk, one launch.
+ * Replaces `_argmax_kernel` (treemoe/kernels/op4_commit.py:82-96) and
+ * `_tree_verify_greedy_kernel` (:99-131) plus the result glue (:223-239).
+ *
+ * logits: [N, V] (row stride `row_stride` elements), dtype TM_DTYPE_F32 or
+ * TM_DTYPE_BF16.  NaN ranks above every number (first NaN wins), as in
+ * torch.argmax.  tokens [N] i64; children in CSR form: child_start [N] i32,
+ * child_count [N] i32, child_list [max(1, N-1)] i32.  The walk visits at most
+ * max_depth levels.
+ * Outputs: argmax [N] i32, accepted_slots [N] i64 (-1 pad), accepted_tokens
+ * [N] i64 (-1 pad), result [3] i64 = (bonus_token, num_accepted, next_root).
+ * `counter` is one u32 of device memory that must be zero before the first
+ * call; the kernel leaves it zero again.
+ */
+int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
+                       int64_t row_stride, const int64_t* tokens,
+                       const int32_t* child_start, const int32_t* child_count,
+                       const int32_t* child_list, int64_t max_depth,
+                       int32_t* argmax, int64_t* accepted_slots,
+                       int64_t* accepted_tokens, int64_t* result,
+                       uint32_t* counter, void* stream);
+
+/*
+ * Paged KV commit of [root] + accepted path.  Replaces `_kv_commit_kernel` and
+ * its host glue (treemoe/kernels/op4_commit.py:134-167, 241-267); reference
+ * semantics `PagedKVCache.commit_tree` (treemoe/model/kv_cache.py:88-106).
+ *
+ * For layer l < L and j <= num_accepted (read on device from result[1]):
+ *   src slot  s = (j == 0 ? 0 : accepted_slots[j-1]),
+ *             page scratch_pages[s / page_size], offset s % page_size;
+ *   dest pos  q = seq_len + j, page block_table[q / page_size], offset q % page_size;
+ *   k[l, dst] = k[l, src] and v[l, dst] = v[l, src], row_bytes bytes each.
+ * k, v: [L, pages, page_size, kvh, hd] with strides (elements of elem_bytes):
+ * stride_layer, stride_page, stride_slot.  Grid covers j <= max_depth.
+ */
+int tm_op4_kv_commit(void* k, void* v, int64_t elem_bytes, int64_t L,
+                     int64_t row_elems, int64_t stride_layer,
+                     int64_t stride_page, int64_t stride_slot,
+                     int64_t page_size, const int64_t* accepted_slots,
+                     const int64_t* result, const int32_t* scratch_pages,
+                     int64_t num_scratch_pages, const int32_t* block_table,
+                     int64_t num_table_pages, int64_t seq_len,
+                     int64_t max_depth, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TREEMOE_AMD_H */

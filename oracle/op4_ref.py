@@ -1,0 +1,83 @@
+"""TEST INFRASTRUCTURE ONLY: restatement of the op4 reference.
+
+* ``tree_verify``  treemoe/ref/verify_ref.py:35-103 (greedy branch exactly;
+  sampling branch with injected uniforms, temperature > 0).  Depth is
+  unbounded, as in the reference.
+* ``commit_tree``  treemoe/model/kv_cache.py:88-106 generalised to a page size
+  P: tree slot s lives in scratch page ``scratch_pages[s // P]`` at offset
+  ``s % P``; sequence position q lives in ``block_table[q // P]`` at ``q % P``.
+"""
+
+from __future__ import annotations
+
+import torch
+
+
+def tree_verify(target_logits: torch.Tensor, draft_probs: torch.Tensor,
+                tree_tokens: torch.Tensor, children: list[list[int]],
+                temperature: float = 0.0, uniforms: torch.Tensor | None = None,
+                generator: torch.Generator | None = None):
+    """Returns (accepted_slots [N], accepted_tokens [N], bonus, num_accepted)."""
+    n = target_logits.shape[0]
+    slots: list[int] = []
+    toks: list[int] = []
+    if temperature != 0.0 and uniforms is None:
+        uniforms = torch.rand(n, generator=generator)
+    node = 0
+    while True:
+        if temperature == 0.0:
+            best = int(target_logits[node].argmax())
+            residual = None
+        else:
+            residual = torch.softmax(target_logits[node] / temperature, dim=-1)
+        taken = -1
+        for c in children[node]:
+            tok = int(tree_tokens[c])
+            if temperature == 0.0:
+                ok = tok == best
+            else:
+                q = draft_probs[c]
+                ratio = (residual[tok] / q[tok].clamp_min(1e-20)).clamp(max=1.0)
+                ok = bool(uniforms[c] < ratio)
+                if not ok:
+                    residual = (residual - q).clamp_min(0)
+                    residual = residual / residual.sum().clamp_min(1e-20)
+            if ok:
+                taken = c
+                break
+        if taken < 0:
+            if temperature == 0.0:
+                bonus = best
+            else:
+                bonus = int(torch.multinomial(residual, 1, generator=generator))
+            break
+        slots.append(taken)
+        toks.append(int(tree_tokens[taken]))
+        node = taken
+    acc_slots = torch.full((n,), -1, dtype=torch.long)
+    acc_toks = torch.full((n,), -1, dtype=torch.long)
+    if slots:
+        acc_slots[: len(slots)] = torch.tensor(slots)
+        acc_toks[: len(toks)] = torch.tensor(toks)
+    return acc_slots, acc_toks, bonus, len(slots)
+
+
+def commit_tree(k: torch.Tensor, v: torch.Tensor, commit_slots: torch.Tensor,
+                scratch_pages: list[int], block_table: list[int], seq_len: int) -> int:
+    """Copy the K/V rows of the valid (>= 0) tree slots in ``commit_slots`` to
+    positions seq_len, seq_len+1, ...; returns the number of rows committed.
+    k, v: [L, pages, P, kvh, hd] (any device, modified in place)."""
+    page = k.shape[2]
+    valid = commit_slots[commit_slots >= 0].tolist()
+    if not valid:
+        return 0
+    src_p = torch.tensor([scratch_pages[s // page] for s in valid], dtype=torch.long)
+    src_o = torch.tensor([s % page for s in valid], dtype=torch.long)
+    pos = [seq_len + j for j in range(len(valid))]
+    dst_p = torch.tensor([block_table[q // page] for q in pos], dtype=torch.long)
+    dst_o = torch.tensor([q % page for q in pos], dtype=torch.long)
+    dev = k.device
+    src_p, src_o, dst_p, dst_o = (t.to(dev) for t in (src_p, src_o, dst_p, dst_o))
+    k[:, dst_p, dst_o] = k[:, src_p, src_o]
+    v[:, dst_p, dst_o] = v[:, src_p, src_o]
+    return len(valid)

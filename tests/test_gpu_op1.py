@@ -1,0 +1,323 @@
+"""op1 parity on the GPU: HIP library vs the CPU oracle.
+
+Bar: routing (expert ids, gate weights, demand, every layout index) is
+bit-exact against the C oracle; the MoE output is within rel-L2 <= 1e-2 of an
+FP64 (small shapes) or FP32 torch (Mixtral shapes) evaluation of the same
+expert FFN with the same routing; outputs are bitwise reproducible.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle_c
+from oracle import op1_ref
+from tests.conftest import bf16_bits, make_moe_inputs
+
+pytestmark = pytest.mark.gpu
+
+REL_L2_TOL = 1e-2
+
+
+def _op1():
+    from treemoe_spec_amd.kernels import op1_tree_moe
+
+    return op1_tree_moe
+
+
+def _say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def _route_case(seed, t, e, h, budget, objective, accept_kind, block_m=16, router_scale=0.1):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(t, h, generator=g).to(torch.bfloat16)
+    router = (torch.randn(e, h, generator=g) * router_scale).to(torch.bfloat16)
+    if accept_kind == "ones":
+        accept = torch.ones(t)
+    elif accept_kind == "zeros":
+        accept = torch.zeros(t)
+    else:
+        accept = torch.rand(t, generator=g)
+    return x, router, accept
+
+
+@pytest.mark.parametrize("t,h,e", [(1, 64, 8), (5, 512, 8), (64, 4096, 8), (64, 256, 2),
+                                   (33, 1024, 16), (2048, 4096, 8), (64, 512, 64)])
+def test_router_gates_bit_exact(t, h, e):
+    _say(f"router t={t} h={h} e={e}")
+    m = _op1()
+    x, router, _ = _route_case(7, t, e, h, 2, "mass", "ones")
+    gates = torch.empty(t, e, dtype=torch.float32, device="cuda")
+    m._launch_router(x.cuda(), router.cuda(), gates)
+    expect = oracle_c.router_gates(bf16_bits(x), bf16_bits(router))
+    got = gates.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
+
+
+ROUTE_CASES = [
+    (seed, t, budget, objective, accept_kind)
+    for seed, t in ((0, 16), (1, 64), (2, 128), (3, 2048), (4, 4096), (5, 7))
+    for budget in (2, 4, 8)
+    for objective in ("mass", "critical_path")
+    for accept_kind in ("ones", "uniform")
+]
+
+
+@pytest.mark.parametrize("seed,t,budget,objective,accept_kind", ROUTE_CASES)
+def test_route_bucket_bit_exact(seed, t, budget, objective, accept_kind):
+    _say(f"route seed={seed} t={t} B={budget} {objective} {accept_kind}")
+    m = _op1()
+    e, h = 8, 256
+    x, router, accept = _route_case(seed, t, e, h, budget, objective, accept_kind)
+    for block_m in (16, 32):
+        got = m.route_and_bucket(x.cuda(), router.cuda(), accept.cuda(), budget,
+                                 block_m=block_m, return_demand=True,
+                                 routing_objective=objective)
+        gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(router))
+        ref = oracle_c.route_bucket(gates, accept.numpy(), budget, objective=objective,
+                                    block_m=block_m)
+        ids, w, padded, blk, s2r, max_blocks, demand = got
+        assert max_blocks == ref.max_blocks
+        assert np.array_equal(ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+        assert np.array_equal(w.reshape(-1).cpu().numpy().view(np.uint32),
+                              ref.gates_flat.view(np.uint32))
+        assert np.array_equal(padded.cpu().numpy(), ref.padded_slots)
+        assert np.array_equal(blk.cpu().numpy(), ref.block_expert_ids)
+        assert np.array_equal(s2r.cpu().numpy(), ref.slot_to_row)
+        assert np.array_equal(demand.cpu().numpy().view(np.uint32), ref.demand.view(np.uint32))
+
+
+@pytest.mark.parametrize("budget", [2, 4, 8])
+@pytest.mark.parametrize("objective", ["mass", "critical_path"])
+def test_route_experts_compact_layout_bit_exact(budget, objective):
+    _say(f"route_experts B={budget} {objective}")
+    m = _op1()
+    t, e, h = 64, 8, 512
+    x, router, accept = _route_case(11, t, e, h, budget, objective, "uniform")
+    r = m.route_experts(x.cuda(), router.cuda(), accept.cuda(), budget, inter=1024,
+                        routing_objective=objective)
+    gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(router))
+    ref = oracle_c.route_bucket(gates, accept.numpy(), budget, objective=objective,
+                                block_m=m.BM)
+    assert np.array_equal(r.router_gates.cpu().numpy().view(np.uint32), gates.view(np.uint32))
+    assert np.array_equal(r.expert_offsets.cpu().numpy(), ref.expert_offsets)
+    assert np.array_equal(r.sorted_slots.cpu().numpy(), ref.sorted_slots)
+    assert np.array_equal(r.slot_pos.cpu().numpy(), ref.slot_pos)
+    assert np.array_equal(r.tiles.cpu().numpy(), ref.tiles)
+    assert r.max_blocks == ref.max_blocks
+    assert r.launch_blocks == m.compact_block_limit(2 * t, budget)
+
+
+@pytest.mark.parametrize("t,budget", [(32, 4), (64, 2), (64, 4), (64, 8), (128, 8), (7, 3)])
+def test_routing_ids_match_reference_algorithm(t, budget):
+    """The device's routing decisions equal the reference's torch algorithm
+    (budget_route_ref) applied to the same gates."""
+    _say(f"ids vs torch reference t={t} B={budget}")
+    m = _op1()
+    e, h = 8, 4096
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(t, h, generator=g, dtype=torch.bfloat16)
+    router = (torch.randn(e, h, generator=g, dtype=torch.bfloat16) * 0.1)
+    accept = torch.rand(t, generator=g)
+    for objective in ("mass", "critical_path"):
+        ids, w, *_ = m.route_and_bucket(x.cuda(), router.cuda(), accept.cuda(), budget,
+                                        routing_objective=objective)
+        gates = torch.from_numpy(oracle_c.router_gates(bf16_bits(x), bf16_bits(router)))
+        ref_ids, ref_w = op1_ref.budget_route(gates, accept, budget,
+                                              routing_objective=objective)
+        ids = ids.cpu()
+        # torch.topk orders exactly equal gates in an implementation-defined
+        # way; the device takes the lower expert id first.  Rows may differ
+        # only by such a swap.
+        for r in (ids != ref_ids).any(1).nonzero().flatten().tolist():
+            a, b = ids[r].tolist()
+            assert ref_ids[r].tolist() == [b, a] and gates[r, a] == gates[r, b] and a < b
+        torch.testing.assert_close(w.cpu(), ref_w, rtol=1e-6, atol=1e-7)
+
+
+def _forward_and_golden(t, e, h, i, budget, seed, objective="mass", accept_kind="uniform"):
+    m = _op1()
+    g = torch.Generator().manual_seed(seed)
+    x, w1, w2, w3, router, accept = make_moe_inputs(t, e, h, i, g, dtype=torch.bfloat16)
+    if accept_kind == "ones":
+        accept = torch.ones(t)
+    dev = [a.cuda() for a in (x, w1, w2, w3, router, accept)]
+    out = m.tree_moe_forward(*dev, budget, routing_objective=objective)
+    gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(router))
+    ref = oracle_c.route_bucket(gates, accept.numpy(), budget, objective=objective)
+    ids = torch.from_numpy(ref.topk_ids).view(t, 2)
+    wts = torch.from_numpy(ref.gates_flat).view(t, 2)
+    golden = op1_ref.expert_ffn_golden(x, w1, w2, w3, ids, wts)
+    return out, golden, (x, w1, w2, w3, router, accept), ref
+
+
+@pytest.mark.parametrize("budget", [2, 4, 8])
+@pytest.mark.parametrize("objective", ["mass", "critical_path"])
+def test_forward_matches_fp64_golden_small(budget, objective):
+    _say(f"forward small B={budget} {objective}")
+    out, golden, inputs, ref = _forward_and_golden(64, 8, 512, 1024, budget, 5, objective)
+    err = op1_ref.rel_l2(out.cpu().float(), golden)
+    assert err <= REL_L2_TOL, err
+    # the reference's own criterion: kernel error <= 2x the bf16 reference's error
+    x, w1, w2, w3, router, accept = inputs
+    routing = (torch.from_numpy(ref.topk_ids).view(-1, 2),
+               torch.from_numpy(ref.gates_flat).view(-1, 2),
+               torch.from_numpy(ref.sorted_slots).long(),
+               torch.from_numpy(ref.expert_offsets).long())
+    bf = op1_ref.tree_moe_forward(x, w1, w2, w3, router, accept, budget, routing=routing)
+    err_out = (out.cpu().double() - golden).abs().max().item()
+    err_ref = (bf.double() - golden).abs().max().item()
+    assert err_out <= 2 * err_ref + 1e-4, (err_out, err_ref)
+
+
+@pytest.mark.parametrize("t", [1, 16, 64, 100, 256])
+def test_forward_token_counts(t):
+    _say(f"forward t={t}")
+    out, golden, _, _ = _forward_and_golden(t, 8, 256, 512, 8, 9)
+    assert op1_ref.rel_l2(out.cpu().float(), golden) <= REL_L2_TOL
+
+
+def test_forward_degrade_branch():
+    _say("forward degrade")
+    m = _op1()
+    g = torch.Generator().manual_seed(17)
+    x, w1, w2, w3, router, _ = make_moe_inputs(64, 8, 256, 512, g, dtype=torch.bfloat16)
+    accept = torch.zeros(64)
+    out = m.tree_moe_forward(x.cuda(), w1.cuda(), w2.cuda(), w3.cuda(), router.cuda(),
+                             accept.cuda(), 8)
+    gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(router))
+    ref = oracle_c.route_bucket(gates, accept.numpy(), 8)
+    assert np.all(ref.gates_flat.reshape(-1, 2)[:, 1] == 0)
+    golden = op1_ref.expert_ffn_golden(x, w1, w2, w3, torch.from_numpy(ref.topk_ids),
+                                       torch.from_numpy(ref.gates_flat))
+    assert op1_ref.rel_l2(out.cpu().float(), golden) <= REL_L2_TOL
+
+
+def test_forward_deterministic_bitwise():
+    _say("forward determinism")
+    m = _op1()
+    g = torch.Generator().manual_seed(11)
+    x, w1, w2, w3, router, accept = make_moe_inputs(64, 8, 1024, 2048, g, dtype=torch.bfloat16)
+    dev = [a.cuda() for a in (x, w1, w2, w3, router, accept)]
+    outs = [m.tree_moe_forward(*dev, 8, deterministic=True).clone() for _ in range(5)]
+    outs.append(m.tree_moe_forward(*dev, 8, deterministic=False).clone())
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+@pytest.mark.parametrize("budget", [2, 8])
+def test_two_phase_equals_inline(budget):
+    _say(f"two-phase B={budget}")
+    m = _op1()
+    g = torch.Generator().manual_seed(21)
+    x, w1, w2, w3, router, accept = make_moe_inputs(64, 8, 512, 1024, g, dtype=torch.bfloat16)
+    dev = [a.cuda() for a in (x, w1, w2, w3, router, accept)]
+    inline = m.tree_moe_forward(*dev, budget).clone()
+    routing = m.route_experts(dev[0], dev[4], dev[5], budget, 1024)
+    ids = routing.expert_ids()
+    assert ids and all(0 <= i < 8 for i in ids) and len(ids) <= budget
+    two = m.tree_moe_forward(*dev, budget, routing=routing)
+    assert torch.equal(inline, two)
+    out = torch.empty_like(dev[0])
+    r = m.tree_moe_forward(*dev, budget, out=out)
+    assert r is out and torch.equal(out, inline)
+
+
+def test_masked_expert_weights_never_read():
+    """NaN-poisoned weights of an expert that no token routes to must not leak
+    (reference tests/test_op1.py:162-170)."""
+    _say("nan poison")
+    m = _op1()
+    g = torch.Generator().manual_seed(1234)
+    x, w1, w2, w3, router, _ = make_moe_inputs(64, 8, 256, 512, g, dtype=torch.float32)
+    x[:, 0] = x[:, 0].abs() + 1.0
+    router[7].zero_()
+    router[7, 0] = -100.0
+    w1[7] = float("nan")
+    w3[7] = float("nan")
+    w2[7] = float("nan")
+    args = [a.to(torch.bfloat16).cuda() for a in (x, w1, w2, w3, router)]
+    out = m.tree_moe_forward(*args, torch.ones(64, device="cuda"), 7)
+    assert not out.isnan().any()
+
+
+def test_exclude_experts_hybrid_matches_full():
+    _say("exclude experts")
+    m = _op1()
+    g = torch.Generator().manual_seed(23)
+    x, w1, w2, w3, router, accept = make_moe_inputs(64, 8, 512, 1024, g, dtype=torch.bfloat16)
+    dev = [a.cuda() for a in (x, w1, w2, w3, router, accept)]
+    full = m.tree_moe_forward(*dev, 4).clone()
+    routing = m.route_experts(dev[0], dev[4], dev[5], 4, 1024)
+    cold = routing.expert_ids()[:2]
+    info = routing.exclude_experts(cold)
+    assert [e for e, _, _ in info] == cold
+    assert not set(routing.expert_ids()) & set(cold)
+    hybrid = m.tree_moe_forward(*dev, 4, routing=routing).float().cpu()
+    for e, toks, gts in info:
+        xe = x[toks].double()
+        y = (torch.nn.functional.silu(xe @ w1[e].double().t()) * (xe @ w3[e].double().t())) \
+            @ w2[e].double().t()
+        hybrid.index_add_(0, toks, (gts.double().unsqueeze(1) * y).float())
+    torch.testing.assert_close(hybrid, full.float().cpu(), rtol=2e-2, atol=5e-2)
+
+
+def _torch_fp32_golden(inp, ids, wts):
+    """Same expert FFN in fp32 torch on the GPU (hipBLASLt), for full shapes."""
+    x = inp.x.float()
+    out = torch.zeros_like(x)
+    t = x.shape[0]
+    ids = ids.view(t, 2).cuda()
+    wts = wts.view(t, 2).cuda()
+    for e in range(inp.w1.shape[0]):
+        sel = ids == e
+        rows = sel.any(1).nonzero().flatten()
+        if rows.numel() == 0:
+            continue
+        gate = (wts * sel.float()).sum(1)[rows]
+        xe = x[rows]
+        h = torch.nn.functional.silu(xe @ inp.w1[e].float().t()) * (xe @ inp.w3[e].float().t())
+        out[rows] += (h @ inp.w2[e].float().t()) * gate.unsqueeze(1)
+    return out
+
+
+@pytest.mark.parametrize("name", ["config2_mixtral_t64_b8", "config3_mixtral_t64_b4_skew",
+                                  "config5_mixtral_t2048_zipf"])
+def test_mixtral_shape_configs(name):
+    _say(f"mixtral {name}")
+    from treemoe_spec_amd.workloads import op1_workload
+
+    m = _op1()
+    inp = op1_workload(name, device="cuda")
+    out = m.tree_moe_forward(inp.x, inp.w1, inp.w2, inp.w3, inp.router, inp.accept,
+                             inp.budget)
+    routing = m.route_experts(inp.x, inp.router, inp.accept, inp.budget, inp.w1.shape[1])
+    gates = oracle_c.router_gates(bf16_bits(inp.x), bf16_bits(inp.router))
+    ref = oracle_c.route_bucket(gates, inp.accept.cpu().numpy(), inp.budget)
+    assert np.array_equal(routing.topk_ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+    assert np.array_equal(routing.gates_flat.cpu().numpy().view(np.uint32),
+                          ref.gates_flat.view(np.uint32))
+    if inp.budget < 8:
+        assert len(routing.expert_ids()) <= inp.budget
+    golden = _torch_fp32_golden(inp, torch.from_numpy(ref.topk_ids),
+                                torch.from_numpy(ref.gates_flat))
+    err = op1_ref.rel_l2(out.float(), golden)
+    _say(f"  rel_l2={err:.3e}")
+    assert err <= REL_L2_TOL
+    again = m.tree_moe_forward(inp.x, inp.w1, inp.w2, inp.w3, inp.router, inp.accept,
+                               inp.budget)
+    assert torch.equal(out, again)
+
+
+def test_rejects_cpu_tensors_and_bad_dtypes():
+    m = _op1()
+    g = torch.Generator().manual_seed(0)
+    x, w1, w2, w3, router, accept = make_moe_inputs(16, 8, 256, 256, g, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        m.tree_moe_forward(x, w1, w2, w3, router, accept, 8)
+    with pytest.raises(TypeError):
+        m.tree_moe_forward(x.float().cuda(), w1.cuda(), w2.cuda(), w3.cuda(), router.cuda(),
+                           accept.cuda(), 8)

@@ -1,0 +1,239 @@
+// op4 on gfx950: first-occurrence argmax over the vocabulary for every tree
+// node, the greedy accept walk (run by the last workgroup to finish its row),
+// and the paged KV commit of [root] + accepted path.
+#include "tm_common.h"
+
+namespace {
+
+constexpr int kArgThreads = 256;
+constexpr int kMaxPath = 2048;
+
+// (va, ia) ranks before (vb, ib): larger value first, NaN above every number,
+// equal values (and NaN vs NaN) go to the lower index.  This is the order in
+// which torch.argmax / numpy.argmax pick their first maximum.
+__device__ __forceinline__ bool tm_ranks_before(float va, int ia, float vb, int ib) {
+  const bool na = va != va;
+  const bool nb = vb != vb;
+  if (na != nb) return na;
+  if (!na && va != vb) return va > vb;
+  return ia < ib;
+}
+
+struct Best {
+  float v;
+  int i;
+  __device__ __forceinline__ void offer(float v2, int i2) {
+    if (tm_ranks_before(v2, i2, v, i)) { v = v2; i = i2; }
+  }
+};
+
+template <int kDtype>
+__device__ __forceinline__ Best scan_row(const void* logits, int64_t row_stride, int row, int V) {
+  Best b{-INFINITY, 0x7fffffff};
+  const int tid = threadIdx.x;
+  if (kDtype == TM_DTYPE_F32) {
+    const float* p = reinterpret_cast<const float*>(logits) + (size_t)row * row_stride;
+    const bool vec = ((uintptr_t)p % 16) == 0;
+    int done = 0;
+    if (vec) {
+      const int nv = V >> 2;
+      const float4* p4 = reinterpret_cast<const float4*>(p);
+      for (int q = tid; q < nv; q += kArgThreads) {
+        const float4 v = p4[q];
+        b.offer(v.x, 4 * q);
+        b.offer(v.y, 4 * q + 1);
+        b.offer(v.z, 4 * q + 2);
+        b.offer(v.w, 4 * q + 3);
+      }
+      done = nv << 2;
+    }
+    for (int q = done + tid; q < V; q += kArgThreads) b.offer(p[q], q);
+  } else {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(logits) + (size_t)row * row_stride;
+    const bool vec = ((uintptr_t)p % 16) == 0;
+    int done = 0;
+    if (vec) {
+      const int nv = V >> 3;
+      const uint4* p8 = reinterpret_cast<const uint4*>(p);
+      for (int q = tid; q < nv; q += kArgThreads) {
+        const uint4 v = p8[q];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          b.offer(__uint_as_float(w[j] << 16), 8 * q + 2 * j);
+          b.offer(__uint_as_float(w[j] & 0xffff0000u), 8 * q + 2 * j + 1);
+        }
+      }
+      done = nv << 3;
+    }
+    for (int q = done + tid; q < V; q += kArgThreads) b.offer(tm_bf16_to_f32(p[q]), q);
+  }
+  return b;
+}
+
+template <int kDtype>
+__global__ void __launch_bounds__(kArgThreads)
+tm_argmax_walk_kernel(const void* __restrict__ logits, int N, int V, int64_t row_stride,
+                      const int64_t* __restrict__ tokens, const int32_t* __restrict__ child_start,
+                      const int32_t* __restrict__ child_count,
+                      const int32_t* __restrict__ child_list, int max_depth,
+                      int32_t* __restrict__ argmax, int64_t* __restrict__ accepted_slots,
+                      int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result,
+                      uint32_t* __restrict__ counter) {
+  __shared__ float s_v[kArgThreads / 64];
+  __shared__ int s_i[kArgThreads / 64];
+  __shared__ int s_last;
+  __shared__ int s_count;
+  __shared__ int s_path[kMaxPath];
+
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  Best b = scan_row<kDtype>(logits, row_stride, row, V);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(b.v, off);
+    const int oi = __shfl_xor(b.i, off);
+    b.offer(ov, oi);
+  }
+  if (lane == 0) {
+    s_v[wave] = b.v;
+    s_i[wave] = b.i;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    Best r{s_v[0], s_i[0]};
+    for (int w = 1; w < kArgThreads / 64; ++w) r.offer(s_v[w], s_i[w]);
+    argmax[row] = r.i;
+    __threadfence();
+    const uint32_t prev = atomicAdd(counter, 1u);
+    s_last = (prev == (uint32_t)(N - 1));
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  // Greedy walk from the root (op4_commit.py:99-131): at each level take the
+  // first child, in child-list order, whose token equals the node's argmax.
+  if (tid == 0) {
+    int node = 0;
+    int count = 0;
+    const int depth = max_depth < kMaxPath ? max_depth : kMaxPath;
+    for (int d = 0; d < depth; ++d) {
+      const int64_t target = (int64_t)__atomic_load_n(argmax + node, __ATOMIC_RELAXED);
+      const int st = child_start[node];
+      const int cnt = child_count[node];
+      int acc = -1;
+      for (int j = 0; j < cnt; ++j) {
+        const int c = child_list[st + j];
+        if (tokens[c] == target) { acc = c; break; }
+      }
+      if (acc < 0) break;
+      s_path[count++] = acc;
+      node = acc;
+    }
+    s_count = count;
+    result[0] = (int64_t)__atomic_load_n(argmax + node, __ATOMIC_RELAXED);
+    result[1] = count;
+    result[2] = node;
+    *counter = 0u;
+  }
+  __syncthreads();
+  const int count = s_count;
+  for (int i = tid; i < N; i += kArgThreads) {
+    const int slot = (i < count) ? s_path[i] : -1;
+    accepted_slots[i] = slot;
+    accepted_tokens[i] = (slot >= 0) ? tokens[slot] : -1;
+  }
+}
+
+// One workgroup per (layer, path position j).  Pure byte copy of one KV row of
+// K and of V from the tree scratch pages to the sequence tail.
+__global__ void __launch_bounds__(256)
+tm_kv_commit_kernel(uint8_t* __restrict__ k, uint8_t* __restrict__ v, int64_t row_bytes,
+                    int64_t stride_layer_b, int64_t stride_page_b, int64_t stride_slot_b,
+                    int64_t page_size, const int64_t* __restrict__ accepted_slots,
+                    const int64_t* __restrict__ result, const int32_t* __restrict__ scratch_pages,
+                    int64_t n_scratch, const int32_t* __restrict__ block_table, int64_t n_table,
+                    int64_t seq_len, int vec16) {
+  const int layer = blockIdx.x;
+  const int j = blockIdx.y;
+  const int64_t num = result[1];
+  if (j > num) return;
+  const int64_t s = (j == 0) ? 0 : accepted_slots[j - 1];
+  if (s < 0 || s / page_size >= n_scratch) return;
+  const int64_t q = seq_len + j;
+  if (q / page_size >= n_table) return;
+  const int64_t sp = scratch_pages[s / page_size];
+  const int64_t dp = block_table[q / page_size];
+  const int64_t src = layer * stride_layer_b + sp * stride_page_b + (s % page_size) * stride_slot_b;
+  const int64_t dst = layer * stride_layer_b + dp * stride_page_b + (q % page_size) * stride_slot_b;
+  if (vec16) {
+    const int64_t n16 = row_bytes >> 4;
+    for (int64_t i = threadIdx.x; i < n16; i += 256) {
+      reinterpret_cast<uint4*>(k + dst)[i] = reinterpret_cast<const uint4*>(k + src)[i];
+      reinterpret_cast<uint4*>(v + dst)[i] = reinterpret_cast<const uint4*>(v + src)[i];
+    }
+  } else {
+    for (int64_t i = threadIdx.x; i < row_bytes; i += 256) {
+      k[dst + i] = k[src + i];
+      v[dst + i] = v[src + i];
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
+                                  int64_t row_stride, const int64_t* tokens,
+                                  const int32_t* child_start, const int32_t* child_count,
+                                  const int32_t* child_list, int64_t max_depth,
+                                  int32_t* argmax, int64_t* accepted_slots,
+                                  int64_t* accepted_tokens, int64_t* result,
+                                  uint32_t* counter, void* stream) {
+  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || max_depth < 0)
+    return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
+  const dim3 grid((unsigned)N);
+  if (dtype == TM_DTYPE_F32) {
+    hipLaunchKernelGGL(tm_argmax_walk_kernel<TM_DTYPE_F32>, grid, dim3(kArgThreads), 0,
+                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, tokens,
+                       child_start, child_count, child_list, (int)max_depth, argmax,
+                       accepted_slots, accepted_tokens, result, counter);
+  } else {
+    hipLaunchKernelGGL(tm_argmax_walk_kernel<TM_DTYPE_BF16>, grid, dim3(kArgThreads), 0,
+                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, tokens,
+                       child_start, child_count, child_list, (int)max_depth, argmax,
+                       accepted_slots, accepted_tokens, result, counter);
+  }
+  TM_HIP_CHECK_LAUNCH();
+  return TM_OK;
+}
+
+extern "C" int tm_op4_kv_commit(void* k, void* v, int64_t elem_bytes, int64_t L,
+                                int64_t row_elems, int64_t stride_layer, int64_t stride_page,
+                                int64_t stride_slot, int64_t page_size,
+                                const int64_t* accepted_slots, const int64_t* result,
+                                const int32_t* scratch_pages, int64_t num_scratch_pages,
+                                const int32_t* block_table, int64_t num_table_pages,
+                                int64_t seq_len, int64_t max_depth, void* stream) {
+  if (L < 1 || L > 65535 || row_elems < 1 || page_size < 1 || max_depth < 0 ||
+      max_depth > 65534 || num_scratch_pages < 1 || num_table_pages < 1 || seq_len < 0)
+    return TM_ERR_SHAPE;
+  if (elem_bytes != 1 && elem_bytes != 2 && elem_bytes != 4 && elem_bytes != 8) return TM_ERR_ARG;
+  if ((seq_len + max_depth) / page_size >= num_table_pages) return TM_ERR_SHAPE;
+  const int64_t row_bytes = row_elems * elem_bytes;
+  const int64_t sl = stride_layer * elem_bytes, sp = stride_page * elem_bytes,
+                ss = stride_slot * elem_bytes;
+  const int vec16 = ((row_bytes % 16) == 0 && (sl % 16) == 0 && (sp % 16) == 0 &&
+                     (ss % 16) == 0 && ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0)
+                        ? 1
+                        : 0;
+  const dim3 grid((unsigned)L, (unsigned)(max_depth + 1));
+  hipLaunchKernelGGL(tm_kv_commit_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+                     (uint8_t*)k, (uint8_t*)v, row_bytes, sl, sp, ss, page_size,
+                     accepted_slots, result, scratch_pages, num_scratch_pages, block_table,
+                     num_table_pages, seq_len, vec16);
+  TM_HIP_CHECK_LAUNCH();
+  return TM_OK;
+}

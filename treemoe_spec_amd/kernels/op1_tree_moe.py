@@ -1,0 +1,344 @@
+"""op1: tree-aware grouped MoE layer (with op3 budget routing) on MI355X.
+
+Same Python surface as the reference module treemoe/kernels/op1_tree_moe.py
+(``compact_block_limit`` :66, ``compact_block_capacity`` :74, ``route_and_bucket``
+:81, ``Routing`` :568, ``route_experts`` :641, ``tree_moe_forward`` :711); the
+work runs in libtreemoe_amd.so:
+
+  router       tm_op1_router_gates   bf16 logits, fp32 softmax
+  routing      tm_op1_route_bucket   budget routing + bucketing, one workgroup
+  gate/up      tm_op1_gemm1          MFMA, SwiGLU fused, h kept in bf16
+  down         tm_op1_gemm2          MFMA, deterministic K split, gate applied
+  combine      tm_op1_combine        fixed order, bf16 output
+
+There is no CPU path: CPU tensors, other dtypes, or a missing library raise.
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from treemoe_spec_amd import _capi
+from treemoe_spec_amd._capi import TM_GEMM_TILE_M, TM_OBJECTIVE, call, ptr
+
+BM = int(os.getenv("TREEMOE_BLOCK_M", "16"))
+if BM not in {16, 32}:
+    raise ValueError("TREEMOE_BLOCK_M must be 16 or 32")
+
+# K segments of the down projection.  Each segment is one deterministic
+# partial; more segments = more workgroups in flight, more partial traffic.
+SPLIT_K = 4
+TILE_M = TM_GEMM_TILE_M
+
+
+def compact_block_limit(num_slots: int, expert_budget: int, block_m: int = BM) -> int:
+    """Tight upper bound on the compact blocks of S slots over <= B experts."""
+    active_upper = min(num_slots, expert_budget)
+    return active_upper + (num_slots - active_upper) // block_m
+
+
+def compact_block_capacity(num_slots: int, expert_budget: int, block_m: int = BM) -> int:
+    """Power-of-two storage capacity for a compact expert-major bucket."""
+    logical = compact_block_limit(num_slots, expert_budget, block_m)
+    return 1 << max(logical - 1, 0).bit_length()
+
+
+def _split_for(inter: int) -> int:
+    for s in (SPLIT_K, 4, 2, 1):
+        if s >= 1 and inter % s == 0 and (inter // s) % 256 == 0:
+            return s
+    raise ValueError("intermediate size must be a multiple of 256")
+
+
+def _check_budget(expert_budget: int, num_experts: int, routing_objective: str) -> None:
+    if not 2 <= expert_budget <= num_experts:
+        raise ValueError(f"expert_budget must be in [2, {num_experts}]")
+    if routing_objective not in TM_OBJECTIVE:
+        raise ValueError("routing_objective must be 'mass' or 'critical_path'")
+
+
+def _require_device(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise RuntimeError(
+                "treemoe_spec_amd op1 runs on ROCm devices only; got a CPU tensor "
+                "(no CPU fallback is provided)")
+
+
+def _require_bf16(name: str, t: torch.Tensor) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be torch.bfloat16, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+class _Workspace:
+    """Static per-shape device buffers, rewritten by every call."""
+
+    def __init__(self, n: int, e: int, hidden: int, inter: int, device, dtype):
+        self.max_blocks = compact_block_capacity(2 * n, e, BM)
+        self.max_tiles = compact_block_limit(2 * n, e, TILE_M)
+        self.num_experts = e
+        self.rows = self.max_blocks * BM
+        self.split = _split_for(inter)
+        i32, i64, f32 = torch.int32, torch.int64, torch.float32
+        self.router_gates = torch.empty(n, e, dtype=f32, device=device)
+        self.h = torch.empty(2 * n, inter, dtype=dtype, device=device)
+        self.partial = torch.zeros(self.split, 2 * n, hidden, dtype=f32, device=device)
+        self.topk_flat = torch.zeros(2 * n, dtype=i64, device=device)
+        self.gates_flat = torch.zeros(2 * n, dtype=f32, device=device)
+        self.padded_slots = torch.full((self.rows,), -1, dtype=i64, device=device)
+        self.block_expert_ids = torch.full((self.max_blocks,), -1, dtype=i64, device=device)
+        self.slot_to_row = torch.zeros(2 * n, dtype=i64, device=device)
+        self.demand = torch.zeros(e, dtype=f32, device=device)
+        self.expert_offsets = torch.zeros(e + 1, dtype=i32, device=device)
+        self.sorted_slots = torch.zeros(2 * n, dtype=i32, device=device)
+        self.slot_pos = torch.zeros(2 * n, dtype=i32, device=device)
+        self.tiles = torch.zeros(self.max_tiles, 4, dtype=i32, device=device)
+
+
+_ws_cache: dict[tuple, _Workspace] = {}
+
+
+def _workspace(n: int, e: int, hidden: int, inter: int, x: torch.Tensor) -> _Workspace:
+    key = (n, e, hidden, inter, x.device.index, x.dtype, BM)
+    ws = _ws_cache.get(key)
+    if ws is None:
+        ws = _ws_cache[key] = _Workspace(n, e, hidden, inter, x.device, x.dtype)
+    return ws
+
+
+def _launch_router(x: torch.Tensor, router_weight: torch.Tensor, gates: torch.Tensor) -> None:
+    n, hidden = x.shape
+    call("tm_op1_router_gates", ptr(x), ptr(router_weight), n, hidden,
+         router_weight.shape[0], ptr(gates), _capi.stream_of(x.device))
+
+
+def _launch_route_bucket(gates, accept, n, e, budget, tau, objective, block_m, max_blocks,
+                         max_tiles, topk, gates_flat, padded, blk, s2r, demand, offsets,
+                         sorted_slots, slot_pos, tiles, device) -> None:
+    call("tm_op1_route_bucket", ptr(gates), ptr(accept), n, e, budget, float(tau),
+         TM_OBJECTIVE[objective], block_m, max_blocks, max_tiles, ptr(topk),
+         ptr(gates_flat), ptr(padded), ptr(blk), ptr(s2r), ptr(demand), ptr(offsets),
+         ptr(sorted_slots), ptr(slot_pos), ptr(tiles), _capi.stream_of(device))
+
+
+def _prep_accept(node_accept_prob: torch.Tensor, n: int) -> torch.Tensor:
+    a = node_accept_prob
+    if a.dtype != torch.float32 or not a.is_contiguous():
+        a = a.float().contiguous()
+    if a.numel() != n:
+        raise ValueError(f"node_accept_prob must have {n} elements, got {a.numel()}")
+    return a
+
+
+def route_and_bucket(
+    x: torch.Tensor,
+    router_weight: torch.Tensor,
+    node_accept_prob: torch.Tensor,
+    expert_budget: int,
+    block_m: int = BM,
+    top1_threshold: float = 0.05,
+    return_demand: bool = False,
+    router_gates: torch.Tensor | None = None,
+    routing_objective: str = "mass",
+):
+    """Returns (topk_ids [N,2], topk_gates [N,2], padded_slots, block_expert_ids,
+    slot_to_row, max_blocks[, demand]) in fresh tensors, like the reference's
+    torch composition (treemoe/kernels/op1_tree_moe.py:81-149)."""
+    _require_device(x, router_weight, node_accept_prob)
+    n = x.shape[0]
+    e = router_weight.shape[0]
+    _check_budget(expert_budget, e, routing_objective)
+    if block_m not in (16, 32):
+        raise ValueError("block_m must be 16 or 32")
+    dev = x.device
+    if router_gates is None:
+        _require_bf16("x", x)
+        _require_bf16("router_weight", router_weight)
+        gates = torch.empty(n, e, dtype=torch.float32, device=dev)
+        _launch_router(x, router_weight, gates)
+    else:
+        gates = router_gates.float().contiguous()
+    accept = _prep_accept(node_accept_prob, n)
+    max_blocks = compact_block_capacity(2 * n, expert_budget, block_m)
+    max_tiles = compact_block_limit(2 * n, expert_budget, TILE_M)
+    i32, i64, f32 = torch.int32, torch.int64, torch.float32
+    topk = torch.empty(2 * n, dtype=i64, device=dev)
+    gflat = torch.empty(2 * n, dtype=f32, device=dev)
+    padded = torch.empty(max_blocks * block_m, dtype=i64, device=dev)
+    blk = torch.empty(max_blocks, dtype=i64, device=dev)
+    s2r = torch.empty(2 * n, dtype=i64, device=dev)
+    demand = torch.empty(e, dtype=f32, device=dev)
+    offsets = torch.empty(e + 1, dtype=i32, device=dev)
+    sorted_slots = torch.empty(2 * n, dtype=i32, device=dev)
+    slot_pos = torch.empty(2 * n, dtype=i32, device=dev)
+    tiles = torch.empty(max_tiles, 4, dtype=i32, device=dev)
+    _launch_route_bucket(gates, accept, n, e, expert_budget, top1_threshold,
+                         routing_objective, block_m, max_blocks, max_tiles, topk, gflat,
+                         padded, blk, s2r, demand, offsets, sorted_slots, slot_pos, tiles, dev)
+    result = (topk.view(n, 2), gflat.view(n, 2), padded, blk, s2r, max_blocks)
+    if return_demand:
+        return (*result, demand)
+    return result
+
+
+class Routing:
+    """Phase-1 result of tree_moe_forward: routing + bucketing, no expert
+    weights touched (reference: treemoe/kernels/op1_tree_moe.py:568-638).
+
+    The reference attributes are views of the workspace; ``expert_offsets``,
+    ``sorted_slots``, ``slot_pos`` and ``tiles`` are the compact layout the
+    GEMMs consume.  A later route_experts() call with the same shape rewrites
+    the workspace, as in the reference."""
+
+    __slots__ = ("ws", "router_gates", "topk_ids", "gates_flat", "padded_slots",
+                 "block_expert_ids", "slot_to_row", "max_blocks", "launch_blocks",
+                 "demand", "expert_offsets", "sorted_slots", "slot_pos", "tiles",
+                 "max_tiles")
+
+    def __init__(self, ws, router_gates, topk_ids, gates_flat, padded_slots,
+                 block_expert_ids, slot_to_row, max_blocks, launch_blocks, demand,
+                 expert_offsets, sorted_slots, slot_pos, tiles, max_tiles):
+        self.ws = ws
+        self.router_gates = router_gates
+        self.topk_ids = topk_ids
+        self.gates_flat = gates_flat
+        self.padded_slots = padded_slots
+        self.block_expert_ids = block_expert_ids
+        self.slot_to_row = slot_to_row
+        self.max_blocks = max_blocks
+        self.launch_blocks = launch_blocks
+        self.demand = demand
+        self.expert_offsets = expert_offsets
+        self.sorted_slots = sorted_slots
+        self.slot_pos = slot_pos
+        self.tiles = tiles
+        self.max_tiles = max_tiles
+
+    def expert_ids(self) -> list[int]:
+        """Experts routed this layer (one small device-to-host copy)."""
+        ids = self.block_expert_ids[: self.launch_blocks].tolist()
+        return sorted({int(i) for i in ids if i >= 0})
+
+    def exclude_experts(self, expert_ids) -> list[tuple[int, torch.Tensor, torch.Tensor]]:
+        """Drop these experts from the device pass and return
+        [(expert, token_idx, gates)] host tensors for a host-side FFN
+        (reference :598-638).  Their GEMM tiles and reference blocks are
+        masked and their partial rows zeroed, so the fixed-order combine adds
+        exact zeros for them."""
+        picked: list[tuple[int, torch.Tensor, torch.Tensor]] = []
+        offsets = self.expert_offsets.tolist()
+        drop = []
+        rows = []
+        for e in expert_ids:
+            e = int(e)
+            lo, hi = offsets[e], offsets[e + 1]
+            if hi <= lo:
+                continue
+            slots = self.sorted_slots[lo:hi].long()
+            picked.append((e, (slots // 2).cpu(), self.gates_flat[slots].float().cpu()))
+            drop.append(e)
+            rows.append(torch.arange(lo, hi, device=slots.device))
+        if not picked:
+            return picked
+        drop_t = torch.tensor(drop, device=self.tiles.device)
+        tile_e = self.tiles[:, 0]
+        self.tiles[:, 0] = torch.where(torch.isin(tile_e.long(), drop_t),
+                                       torch.full_like(tile_e, -1), tile_e)
+        blk = self.block_expert_ids
+        blk[torch.isin(blk, drop_t)] = -1
+        self.ws.partial[:, torch.cat(rows)] = 0.0
+        return picked
+
+
+def route_experts(
+    x: torch.Tensor,
+    router_weight: torch.Tensor,
+    node_accept_prob: torch.Tensor,
+    expert_budget: int,
+    inter: int,
+    top1_threshold: float = 0.05,
+    routing_objective: str = "mass",
+) -> Routing:
+    """Phase 1 of tree_moe_forward: router + op3 budget routing + bucketing.
+    Reads only the router weights; ``inter`` is the FFN size (sizes the
+    workspace)."""
+    _check_budget(expert_budget, router_weight.shape[0], routing_objective)
+    _require_device(x, router_weight, node_accept_prob)
+    _require_bf16("x", x)
+    _require_bf16("router_weight", router_weight)
+    n, hidden = x.shape
+    e = router_weight.shape[0]
+    if router_weight.shape[1] != hidden:
+        raise ValueError("router_weight must be [E, H] with H = x.shape[1]")
+    ws = _workspace(n, e, hidden, inter, x)
+    accept = _prep_accept(node_accept_prob, n)
+    max_blocks = compact_block_capacity(2 * n, expert_budget, BM)
+    launch_blocks = compact_block_limit(2 * n, expert_budget, BM)
+    max_tiles = compact_block_limit(2 * n, expert_budget, TILE_M)
+    _launch_router(x, router_weight, ws.router_gates)
+    padded = ws.padded_slots[: max_blocks * BM]
+    blk = ws.block_expert_ids[:max_blocks]
+    tiles = ws.tiles[:max_tiles]
+    _launch_route_bucket(ws.router_gates, accept, n, e, expert_budget, top1_threshold,
+                         routing_objective, BM, max_blocks, max_tiles, ws.topk_flat,
+                         ws.gates_flat, padded, blk, ws.slot_to_row, ws.demand,
+                         ws.expert_offsets, ws.sorted_slots, ws.slot_pos, tiles, x.device)
+    return Routing(ws, ws.router_gates, ws.topk_flat.view(n, 2), ws.gates_flat, padded, blk,
+                   ws.slot_to_row, max_blocks, launch_blocks, ws.demand, ws.expert_offsets,
+                   ws.sorted_slots, ws.slot_pos, tiles, max_tiles)
+
+
+def tree_moe_forward(
+    x: torch.Tensor,
+    w1: torch.Tensor,
+    w2: torch.Tensor,
+    w3: torch.Tensor,
+    router_weight: torch.Tensor,
+    node_accept_prob: torch.Tensor,
+    expert_budget: int,
+    out: torch.Tensor | None = None,
+    deterministic: bool = True,
+    routing: Routing | None = None,
+    routing_objective: str = "mass",
+) -> torch.Tensor:
+    """op1 entry point (reference :711-802).
+
+    Always bitwise deterministic: the down projection writes K-split partials
+    and the combine sums them in a fixed order, so ``deterministic=False``
+    (the reference's atomic variant) returns the same bits.  ``routing`` is a
+    precomputed phase-1 handle from route_experts(); None routes inline."""
+    _check_budget(expert_budget, router_weight.shape[0], routing_objective)
+    _require_device(x, w1, w2, w3, router_weight, node_accept_prob)
+    for name, t in (("x", x), ("w1", w1), ("w2", w2), ("w3", w3)):
+        _require_bf16(name, t)
+    n, hidden = x.shape
+    e, inter, h_w = w1.shape
+    if h_w != hidden or w3.shape != w1.shape or tuple(w2.shape) != (e, hidden, inter):
+        raise ValueError("expected w1, w3 [E, I, H] and w2 [E, H, I] matching x [T, H]")
+    if hidden % 256 != 0 or inter % 256 != 0:
+        raise ValueError("hidden and intermediate sizes must be multiples of 256")
+    if routing is None:
+        routing = route_experts(x, router_weight, node_accept_prob, expert_budget, inter,
+                                routing_objective=routing_objective)
+    ws = routing.ws
+    if ws.h.shape != (2 * n, inter) or ws.partial.shape[2] != hidden:
+        raise ValueError("routing was computed for a different shape")
+    stream = _capi.stream_of(x.device)
+    call("tm_op1_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h), ptr(routing.sorted_slots),
+         ptr(routing.tiles), routing.max_tiles, n, hidden, inter, e, stream)
+    call("tm_op1_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial), ptr(routing.gates_flat),
+         ptr(routing.sorted_slots), ptr(routing.tiles), routing.max_tiles, ws.split, n,
+         hidden, inter, e, stream)
+    if out is not None:
+        if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+            raise ValueError("out must be a contiguous tensor like x")
+        result = out
+    else:
+        result = torch.empty_like(x)
+    call("tm_op1_combine", ptr(ws.partial), ptr(routing.slot_pos), ptr(result), n, hidden,
+         ws.split, stream)
+    return result

@@ -1,0 +1,115 @@
+"""Paged KV cache consumed by op4's commit (reference: treemoe/model/kv_cache.py).
+
+Layout per tensor: [layers, pages, page_size, kv_heads, head_dim].  The first
+``ceil(tree_size / page_size)`` pages are the tree scratch: tree slot s lives in
+page ``tree_pages[s // page_size]`` at offset ``s % page_size`` (with the
+reference's page size 64 and a 64-node tree this is the single page 0,
+``tree_block``).  Sequence position q lives in ``block_table[q // page_size]``
+at offset ``q % page_size`` (reference ``slot_of``, :57-58).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+BLOCK_SIZE = 64
+
+
+@dataclass(frozen=True)
+class MixtralConfig:
+    """Mixtral-8x7B dimensions (reference: treemoe/model/config.py:10-29)."""
+
+    num_layers: int = 32
+    num_experts: int = 8
+    top_k: int = 2
+    hidden_dim: int = 4096
+    intermediate_dim: int = 14336
+    num_heads: int = 32
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    vocab_size: int = 32000
+    rope_theta: float = 1e6
+    rms_eps: float = 1e-5
+    max_seq_len: int = 8192
+    dtype: torch.dtype = torch.bfloat16
+
+    @property
+    def expert_bytes_per_layer(self) -> int:
+        return 3 * self.intermediate_dim * self.hidden_dim * 2
+
+
+class PagedKVCache:
+    def __init__(self, config, num_blocks: int, device: str = "cuda",
+                 dtype: torch.dtype = torch.bfloat16, page_size: int = BLOCK_SIZE,
+                 tree_size: int = 64):
+        self.config = config
+        self.block_size = page_size
+        n_scratch = (tree_size + page_size - 1) // page_size
+        if num_blocks <= n_scratch:
+            raise ValueError("num_blocks must exceed the tree scratch pages")
+        shape = (config.num_layers, num_blocks, page_size, config.num_kv_heads,
+                 config.head_dim)
+        self.k = torch.zeros(shape, device=device, dtype=dtype)
+        self.v = torch.zeros(shape, device=device, dtype=dtype)
+        self.block_table: list[int] = []
+        self.seq_len = 0
+        self.tree_pages = list(range(n_scratch))
+        self.tree_block = self.tree_pages[0]
+        self.tree_size = tree_size
+        self._free = list(range(num_blocks - 1, n_scratch - 1, -1))
+        self._dev_table: torch.Tensor | None = None
+        self._dev_table_len = -1
+        self._dev_scratch: torch.Tensor | None = None
+
+    def reset(self) -> None:
+        """Start a new sequence without clearing the backing tensors."""
+        self._free.extend(reversed(self.block_table))
+        self.block_table.clear()
+        self.seq_len = 0
+        self._dev_table_len = -1
+
+    def _ensure_capacity(self, new_len: int) -> None:
+        while len(self.block_table) * self.block_size < new_len:
+            if not self._free:
+                raise RuntimeError("KV cache out of blocks")
+            self.block_table.append(self._free.pop())
+
+    def slot_of(self, pos: int) -> tuple[int, int]:
+        return self.block_table[pos // self.block_size], pos % self.block_size
+
+    def write_tree(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Write the KV rows of tree nodes 0..n-1 into the scratch pages."""
+        n = k.shape[0]
+        if n > len(self.tree_pages) * self.block_size:
+            raise ValueError("tree larger than the scratch pages")
+        for i, page in enumerate(self.tree_pages):
+            lo = i * self.block_size
+            hi = min(n, lo + self.block_size)
+            if hi <= lo:
+                break
+            self.k[layer, page, : hi - lo] = k[lo:hi]
+            self.v[layer, page, : hi - lo] = v[lo:hi]
+
+    def device_tables(self, device) -> tuple[torch.Tensor, torch.Tensor]:
+        """int32 copies of block_table and the scratch page list on ``device``,
+        refreshed only when the block table has grown."""
+        if self._dev_table is None or self._dev_table_len != len(self.block_table) \
+                or self._dev_table.device != torch.device(device):
+            self._dev_table = torch.tensor(self.block_table or [0], dtype=torch.int32,
+                                           device=device)
+            self._dev_table_len = len(self.block_table)
+        if self._dev_scratch is None or self._dev_scratch.device != torch.device(device):
+            self._dev_scratch = torch.tensor(self.tree_pages, dtype=torch.int32, device=device)
+        return self._dev_table, self._dev_scratch
+
+    def gather(self, layer: int, upto: int | None = None):
+        """Contiguous [T, kv_heads, head_dim] K and V of positions 0..T-1."""
+        t = self.seq_len if upto is None else upto
+        nblk = (t + self.block_size - 1) // self.block_size
+        idx = torch.tensor(self.block_table[:nblk], device=self.k.device, dtype=torch.long)
+        kvh, hd = self.k.shape[3], self.k.shape[4]
+        k = self.k[layer, idx].reshape(nblk * self.block_size, kvh, hd)[:t]
+        v = self.v[layer, idx].reshape(nblk * self.block_size, kvh, hd)[:t]
+        return k, v
