@@ -1,0 +1,84 @@
+"""CPU: libtreemoe_amd.so loads, exports every entry point declared in
+include/treemoe_amd.h, and rejects bad arguments before touching the GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "treemoe_amd.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return re.findall(r"^\s*(?:const\s+)?\w+\s*\**\s*(tm_\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for n in ("tm_version", "tm_status_string", "tm_op1_router_gates", "tm_op1_route_bucket",
+              "tm_op1_gemm1", "tm_op1_gemm2", "tm_op1_combine", "tm_op4_argmax_walk",
+              "tm_op4_kv_commit"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from treemoe_spec_amd import _capi
+
+    lib = _capi.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(_capi.SIGNATURES) <= set(declared_functions())
+    assert lib.tm_version() == 100
+
+
+def test_status_strings():
+    from treemoe_spec_amd import _capi
+
+    lib = _capi.lib()
+    assert lib.tm_status_string(0) == b"ok"
+    for code in (1001, 1002, 1003):
+        assert lib.tm_status_string(code) not in (b"ok", b"unknown status")
+
+
+@pytest.mark.parametrize("call,expect", [
+    (("tm_op1_router_gates", 0, 0, 0, 4096, 8, 0, 0), 1001),          # T = 0
+    (("tm_op1_router_gates", 0, 0, 4, 4095, 8, 0, 0), 1001),          # H % 8
+    (("tm_op1_router_gates", 0, 0, 4, 4096, 65, 0, 0), 1001),         # E > 64
+    (("tm_op1_router_gates", 8, 0, 4, 4096, 8, 0, 0), 1002),          # unaligned x
+    (("tm_op1_gemm1", 0, 0, 0, 0, 0, 0, 1, 64, 4000, 14336, 8, 0), 1001),  # H % 256
+    (("tm_op1_gemm2", 0, 0, 0, 0, 0, 0, 1, 3, 64, 4096, 14336, 8, 0), 1001),  # split
+    (("tm_op1_combine", 0, 0, 0, 64, 4094, 2, 0), 1001),
+    (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1003),
+    (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1001),
+])
+def test_argument_errors_return_before_launch(call, expect):
+    from treemoe_spec_amd import _capi
+
+    name, *args = call
+    fn = getattr(_capi.lib(), name)
+    assert fn(*args) == expect
+
+
+def test_route_bucket_argument_errors():
+    from treemoe_spec_amd import _capi
+
+    fn = _capi.lib().tm_op1_route_bucket
+    base = [0, 0, 64, 8, 4, ctypes.c_float(0.05), 0, 16, 16, 11] + [0] * 11
+    args = list(base)
+    args[4] = 9          # budget > E
+    assert fn(*args) == 1003
+    args = list(base)
+    args[6] = 5          # objective
+    assert fn(*args) == 1003
+    args = list(base)
+    args[7] = 8          # block_m
+    assert fn(*args) == 1003
+    args = list(base)
+    args[8] = 4096       # padded rows beyond the workgroup's table
+    assert fn(*args) == 1001

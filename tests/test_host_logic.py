@@ -1,0 +1,125 @@
+"""CPU: host-side logic of the package (validation, layouts, workspaces,
+KV-cache bookkeeping, synthetic workloads).  No GPU work is launched."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from tests.conftest import make_moe_inputs
+
+
+def test_budget_and_objective_validation_messages():
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+
+    g = torch.Generator().manual_seed(0)
+    x, w1, w2, w3, router, accept = make_moe_inputs(8, 4, 256, 256, g, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match=r"expert_budget must be in \[2, 4\]"):
+        m.tree_moe_forward(x, w1, w2, w3, router, accept, 5)
+    with pytest.raises(ValueError, match="routing_objective"):
+        m.route_experts(x, router, accept, 2, 256, routing_objective="x")
+
+
+def test_cpu_tensors_fail_loudly():
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+    from treemoe_spec_amd.kernels import op4_commit as o
+
+    g = torch.Generator().manual_seed(0)
+    x, w1, w2, w3, router, accept = make_moe_inputs(8, 4, 256, 256, g, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        m.tree_moe_forward(x, w1, w2, w3, router, accept, 2)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        m.route_and_bucket(x, router, accept, 2)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        o.fused_verify_commit(torch.zeros(2, 8), None, torch.zeros(2), None, [[1], []])
+    with pytest.raises(NotImplementedError):
+        o.fused_verify_commit(torch.zeros(2, 8), None, torch.zeros(2), None, [[1], []],
+                              temperature=0.7)
+
+
+def test_block_m_env_is_validated(monkeypatch):
+    import importlib
+
+    import treemoe_spec_amd.kernels.op1_tree_moe as m
+
+    monkeypatch.setenv("TREEMOE_BLOCK_M", "24")
+    with pytest.raises(ValueError, match="TREEMOE_BLOCK_M"):
+        importlib.reload(m)
+    monkeypatch.setenv("TREEMOE_BLOCK_M", "16")
+    importlib.reload(m)
+
+
+def test_workspace_kat():
+    """Reference KAT tests/test_op1.py:377-391: T=64 -> 16 blocks, 15 launched,
+    256 padded rows (BM16)."""
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+
+    assert m.compact_block_capacity(128, 8, 16) == 16
+    assert m.compact_block_limit(128, 8, 16) == 15
+    assert m.compact_block_capacity(128, 8, 16) * 16 == 256
+    assert m.compact_block_limit(128, 8, m.TILE_M) == 9
+
+
+@pytest.mark.parametrize("inter,split", [(14336, 4), (3584, 2), (512, 2), (1024, 4), (256, 1)])
+def test_split_selection(inter, split):
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+
+    assert m._split_for(inter) == split
+    with pytest.raises(ValueError):
+        m._split_for(200)
+
+
+def test_children_csr_packing():
+    from treemoe_spec_amd.kernels.op4_commit import _children_csr
+
+    children = [[1, 2], [3], [], []]
+    csr = _children_csr(children, 4, "cpu").tolist()
+    assert csr[:4] == [0, 2, 3, 3] and csr[4:8] == [2, 1, 0, 0] and csr[8:] == [1, 2, 3]
+    with pytest.raises(ValueError):
+        _children_csr([[5], [], [], []], 4, "cpu")
+    with pytest.raises(ValueError):
+        _children_csr([[1]], 4, "cpu")
+
+
+def test_kv_cache_bookkeeping_page16():
+    from treemoe_spec_amd.kv_cache import MixtralConfig, PagedKVCache
+
+    cfg = MixtralConfig(num_layers=2, num_kv_heads=2, head_dim=8)
+    kv = PagedKVCache(cfg, 12, device="cpu", dtype=torch.float32, page_size=16, tree_size=64)
+    assert kv.tree_pages == [0, 1, 2, 3] and kv.tree_block == 0
+    kv._ensure_capacity(40)
+    assert len(kv.block_table) == 3 and all(p >= 4 for p in kv.block_table)
+    assert kv.slot_of(17) == (kv.block_table[1], 1)
+    with pytest.raises(RuntimeError, match="out of blocks"):
+        kv._ensure_capacity(16 * 9)
+    kv.reset()
+    assert kv.seq_len == 0 and kv.block_table == []
+    k = torch.randn(50, 2, 8)
+    kv.write_tree(1, k, k + 1)
+    assert torch.equal(kv.k[1, 1, :16], k[16:32]) and torch.equal(kv.v[1, 3, :2], k[48:50] + 1)
+
+
+def test_kv_cache_reference_layout():
+    from treemoe_spec_amd.kv_cache import BLOCK_SIZE, MixtralConfig, PagedKVCache
+
+    kv = PagedKVCache(MixtralConfig(num_layers=1, num_kv_heads=1, head_dim=4), 4,
+                      device="cpu", dtype=torch.float32)
+    assert kv.block_size == BLOCK_SIZE == 64 and kv.tree_pages == [0]
+    kv._ensure_capacity(65)
+    assert kv.block_table == [1, 2]
+
+
+def test_workloads_are_seeded():
+    from treemoe_spec_amd.workloads import draw_activations, op4_workload
+
+    a = draw_activations(8, 64, 8, 2, "normal1.5")
+    b = draw_activations(8, 64, 8, 2, "normal1.5")
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    assert torch.all(a[0][:, 0] == 1.0)
+    w1 = op4_workload(n=32, vocab=500, max_depth=4, seed=9)
+    w2 = op4_workload(n=32, vocab=500, max_depth=4, seed=9)
+    assert torch.equal(w1.logits, w2.logits) and w1.children == w2.children
+    assert max(w1.depth) <= 4
+    for node, kids in enumerate(w1.children):
+        toks = [int(w1.tokens[c]) for c in kids]
+        assert len(toks) == len(set(toks)) and all(c > node for c in kids)
