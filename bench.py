@@ -36,6 +36,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="time budget of the CPU-baseline sample (0 disables it)")
     p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--copy-probe-mb", type=int, default=0,
+                   help="run one plain device copy of this many MiB first (a known-size "
+                        "reference for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
     return p.parse_args()
 
 
@@ -151,6 +154,14 @@ def main():
     from treemoe_spec_amd.workloads import (op1_algorithmic_bytes, op1_flops, op1_workload)
 
     torch.cuda.set_device(0)
+    if args.copy_probe_mb > 0:
+        src = torch.ones(args.copy_probe_mb << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy probe: {args.copy_probe_mb} MiB device-to-device")
+        del src, dst
     log("drawing config 2 inputs")
     inp = op1_workload("config2_mixtral_t64_b8", device="cuda")
     t, h, i, e = inp.shape
