@@ -65,6 +65,21 @@ def test_argument_errors_return_before_launch(call, expect):
     assert fn(*args) == expect
 
 
+def test_fused_route_argument_errors():
+    from treemoe_spec_amd import _capi
+
+    fn = _capi.lib().tm_op1_route
+    # x = 8 is misaligned, so every case below fails a check before any launch
+    base = [8, 0, 0, 64, 4096, 8, 4, ctypes.c_float(0.05), 0, 16, 16, 11] + [0] * 13
+    assert fn(*base) == 1002
+    args = list(base)
+    args[4] = 4095
+    assert fn(*args) == 1001                 # H % 8
+    args = list(base)
+    args[6] = 1
+    assert fn(*args) == 1003                 # budget < 2
+
+
 def test_route_bucket_argument_errors():
     from treemoe_spec_amd import _capi
 

@@ -90,6 +90,47 @@ def test_route_bucket_bit_exact(seed, t, budget, objective, accept_kind):
         assert np.array_equal(demand.cpu().numpy().view(np.uint32), ref.demand.view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [7, 64, 2048])
+@pytest.mark.parametrize("budget", [2, 4, 8])
+def test_bucket_from_given_gates_bit_exact(t, budget):
+    """route_and_bucket(router_gates=...) runs the bucketing alone (the
+    reference's Kernel A input contract, op1_tree_moe.py:159-190)."""
+    _say(f"bucket from gates t={t} B={budget}")
+    m = _op1()
+    g = torch.Generator().manual_seed(t + budget)
+    gates = torch.softmax(torch.randn(t, 8, generator=g) * 2, -1)
+    accept = torch.rand(t, generator=g)
+    x = torch.zeros(t, 256, dtype=torch.bfloat16)
+    router = torch.zeros(8, 256, dtype=torch.bfloat16)
+    for objective in ("mass", "critical_path"):
+        ids, w, padded, blk, s2r, max_blocks, demand = m.route_and_bucket(
+            x.cuda(), router.cuda(), accept.cuda(), budget, return_demand=True,
+            router_gates=gates.cuda(), routing_objective=objective)
+        ref = oracle_c.route_bucket(gates.numpy(), accept.numpy(), budget, objective=objective)
+        assert np.array_equal(ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+        assert np.array_equal(w.reshape(-1).cpu().numpy().view(np.uint32),
+                              ref.gates_flat.view(np.uint32))
+        assert np.array_equal(padded.cpu().numpy(), ref.padded_slots)
+        assert np.array_equal(blk.cpu().numpy(), ref.block_expert_ids)
+        assert np.array_equal(s2r.cpu().numpy(), ref.slot_to_row)
+        assert np.array_equal(demand.cpu().numpy().view(np.uint32), ref.demand.view(np.uint32))
+
+
+def test_fused_route_repeated_calls_reset_counter():
+    """The fused routing launch leaves its completion counter at zero, so
+    back-to-back calls of different sizes stay correct."""
+    _say("fused route repeated")
+    m = _op1()
+    for t in (64, 5, 64, 300, 1):
+        x, router, accept = _route_case(t, t, 8, 512, 4, "mass", "uniform")
+        r = m.route_experts(x.cuda(), router.cuda(), accept.cuda(), 4, inter=512)
+        gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(router))
+        ref = oracle_c.route_bucket(gates, accept.numpy(), 4)
+        assert np.array_equal(r.topk_ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+        assert np.array_equal(r.tiles.cpu().numpy(), ref.tiles)
+    assert int(r.ws.counter.item()) == 0
+
+
 @pytest.mark.parametrize("budget", [2, 4, 8])
 @pytest.mark.parametrize("objective", ["mass", "critical_path"])
 def test_route_experts_compact_layout_bit_exact(budget, objective):

@@ -4,14 +4,19 @@
 // Every floating-point operation here is written out in a fixed order with
 // contraction disabled, so that the CPU restatement reproduces the outputs bit
 // for bit: expert ids, gate weights, demand and every layout index.
+//
+// Launch shapes: the router runs one workgroup (8 waves) per token, one wave
+// per expert.  The bucketing runs in one workgroup; in the fused entry point
+// it is the last router workgroup to finish (a device-scope counter that the
+// kernel returns to zero), so routing costs a single launch.
 #pragma clang fp contract(off)
 
 #include "tm_common.h"
 
 namespace {
 
-constexpr int kRouteThreads = 1024;
-constexpr int kRouteWaves = kRouteThreads / 64;
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSlots = 2 * TM_MAX_TOKENS;
 constexpr int kMaxChunks = kMaxSlots / 64;
 constexpr int kMaxPaddedRows = 16384;
@@ -19,52 +24,94 @@ constexpr int kMaxPaddedRows = 16384;
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// One wave per token.  Lane l accumulates the 8-element chunks l, l+64, ... of
-// the dot product in element order (fmaf of exact bf16 products), the 64 lane
-// sums are combined by a halving tree (xor butterfly), and the sum is rounded
-// to bf16 like the output of F.linear on bf16 operands
-// (treemoe/kernels/op1_tree_moe.py:676).  Softmax (:677) then runs in fp32:
-// max, e^(l - max), a sum in expert order, and a correctly rounded division.
-__global__ void __launch_bounds__(256)
-tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
-                 float* __restrict__ gates, int T, int H, int E) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + wave;
-  if (t >= T) return;
-  const int nchunk = H >> 3;
-  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)t * H);
-  float my_logit = 0.0f;
-  for (int e = 0; e < E; ++e) {
-    const uint4* wr = reinterpret_cast<const uint4*>(wg + (size_t)e * H);
-    float acc = 0.0f;
-    for (int c = lane; c < nchunk; c += 64) {
-      const uint4 xv = xr[c];
-      const uint4 wv = wr[c];
-      acc = fmaf(lo_bf16(xv.x), lo_bf16(wv.x), acc);
-      acc = fmaf(hi_bf16(xv.x), hi_bf16(wv.x), acc);
-      acc = fmaf(lo_bf16(xv.y), lo_bf16(wv.y), acc);
-      acc = fmaf(hi_bf16(xv.y), hi_bf16(wv.y), acc);
-      acc = fmaf(lo_bf16(xv.z), lo_bf16(wv.z), acc);
-      acc = fmaf(hi_bf16(xv.z), hi_bf16(wv.z), acc);
-      acc = fmaf(lo_bf16(xv.w), lo_bf16(wv.w), acc);
-      acc = fmaf(hi_bf16(xv.w), hi_bf16(wv.w), acc);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
-    const float logit = tm_bf16_to_f32(tm_f32_to_bf16(acc));
-    if (lane == e) my_logit = logit;
-  }
-  float m = (lane < E) ? my_logit : -INFINITY;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-  const float ex = (lane < E) ? tm_expf_det(my_logit - m) : 0.0f;
-  float s = 0.0f;
-  for (int e = 0; e < E; ++e) s = s + __shfl(ex, e);
-  if (lane < E) gates[(size_t)t * E + lane] = ex / s;
+__device__ __forceinline__ float fma8(uint4 xv, uint4 wv, float acc) {
+  acc = fmaf(lo_bf16(xv.x), lo_bf16(wv.x), acc);
+  acc = fmaf(hi_bf16(xv.x), hi_bf16(wv.x), acc);
+  acc = fmaf(lo_bf16(xv.y), lo_bf16(wv.y), acc);
+  acc = fmaf(hi_bf16(xv.y), hi_bf16(wv.y), acc);
+  acc = fmaf(lo_bf16(xv.z), lo_bf16(wv.z), acc);
+  acc = fmaf(hi_bf16(xv.z), hi_bf16(wv.z), acc);
+  acc = fmaf(lo_bf16(xv.w), lo_bf16(wv.w), acc);
+  acc = fmaf(hi_bf16(xv.w), hi_bf16(wv.w), acc);
+  return acc;
 }
 
-// Budget routing and bucketing for all T tokens in one workgroup of 16 waves.
+// Router for token t in one workgroup.  Logit (t, e): lane l of the wave that
+// owns expert e accumulates the 8-element chunks l, l+64, ... in element order
+// (fmaf of exact bf16 products); the 64 lane sums are combined by a halving
+// tree (xor butterfly) and rounded to bf16, as F.linear on bf16 operands
+// returns (treemoe/kernels/op1_tree_moe.py:676).  Softmax (:677) in fp32: max,
+// e^(l - max), a sum in expert order, a correctly rounded division.
+__device__ __forceinline__ void router_token(const uint16_t* __restrict__ x,
+                                             const uint16_t* __restrict__ wg,
+                                             float* __restrict__ gates, int t, int H, int E,
+                                             float* s_logit) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int nchunk = H >> 3;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)t * H);
+  for (int e = wave; e < E; e += kWaves) {
+    const uint4* wr = reinterpret_cast<const uint4*>(wg + (size_t)e * H);
+    float acc = 0.0f;
+    int c = lane;
+    for (; c + 64 * 7 < nchunk; c += 64 * 8) {
+      uint4 xv[8], wv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        xv[u] = xr[c + 64 * u];
+        wv[u] = wr[c + 64 * u];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = fma8(xv[u], wv[u], acc);
+    }
+    for (; c < nchunk; c += 64) acc = fma8(xr[c], wr[c], acc);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
+    if (lane == 0) s_logit[e] = tm_bf16_to_f32(tm_f32_to_bf16(acc));
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const float my_logit = (lane < E) ? s_logit[lane] : 0.0f;
+    float m = (lane < E) ? my_logit : -INFINITY;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    const float ex = (lane < E) ? tm_expf_det(my_logit - m) : 0.0f;
+    float s = 0.0f;
+    for (int e = 0; e < E; ++e) s = s + __shfl(ex, e);
+    if (lane < E) gates[(size_t)t * E + lane] = ex / s;
+  }
+}
+
+struct BucketArgs {
+  const float* gates;
+  const float* accept;
+  int T, E, budget, objective, BM, max_blocks, max_tiles;
+  float tau;
+  int64_t* topk_ids;
+  float* gates_flat;
+  int64_t* padded_slots;
+  int64_t* block_expert_ids;
+  int64_t* slot_to_row;
+  float* demand_out;
+  int32_t* expert_offsets;
+  int32_t* sorted_slots;
+  int32_t* slot_pos;
+  int32_t* tiles;
+};
+
+struct BucketShared {
+  float demand[TM_MAX_EXPERTS];
+  float crit[TM_MAX_EXPERTS];
+  int keep[TM_MAX_EXPERTS];
+  int count[TM_MAX_EXPERTS];
+  int block_start[TM_MAX_EXPERTS];
+  int nblocks[TM_MAX_EXPERTS];
+  int offset[TM_MAX_EXPERTS + 1];
+  uint8_t fe[kMaxSlots];
+  uint16_t cnt[kMaxChunks * TM_MAX_EXPERTS];
+};
+
+// Budget routing and bucketing for all T tokens in one workgroup.
 //
 //  1. demand[e] = sum_t accept[t] * gates[t, e]: lane l of the wave that owns
 //     expert e sums tokens l, l+64, ... in order, then a halving tree
@@ -79,37 +126,19 @@ tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg
 //  4. slot s = 2t + k; stable rank inside its expert from wave ballots; the
 //     reference's padded BM-row block layout (op1_tree_moe.py:111-144) and the
 //     compact expert-major order with its GEMM tile list.
-__global__ void __launch_bounds__(kRouteThreads)
-tm_route_bucket_kernel(const float* __restrict__ gates, const float* __restrict__ accept,
-                       int T, int E, int budget, float tau, int objective, int BM,
-                       int max_blocks, int max_tiles, int64_t* __restrict__ topk_ids,
-                       float* __restrict__ gates_flat, int64_t* __restrict__ padded_slots,
-                       int64_t* __restrict__ block_expert_ids, int64_t* __restrict__ slot_to_row,
-                       float* __restrict__ demand_out, int32_t* __restrict__ expert_offsets,
-                       int32_t* __restrict__ sorted_slots, int32_t* __restrict__ slot_pos,
-                       int32_t* __restrict__ tiles) {
-  __shared__ float s_demand[TM_MAX_EXPERTS];
-  __shared__ float s_crit[TM_MAX_EXPERTS];
-  __shared__ int s_keep[TM_MAX_EXPERTS];
-  __shared__ int s_count[TM_MAX_EXPERTS];
-  __shared__ int s_block_start[TM_MAX_EXPERTS];
-  __shared__ int s_nblocks[TM_MAX_EXPERTS];
-  __shared__ int s_offset[TM_MAX_EXPERTS + 1];
-  __shared__ uint8_t s_fe[kMaxSlots];
-  __shared__ uint16_t s_cnt[kMaxChunks * TM_MAX_EXPERTS];
-  __shared__ int16_t s_padded[kMaxPaddedRows];
-
+__device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
+  const int T = a.T, E = a.E;
   const int nslot = 2 * T;
   const int nchunk = (nslot + 63) >> 6;
-  const int padded_rows = max_blocks * BM;
+  const int padded_rows = a.max_blocks * a.BM;
+  const bool critical = a.objective == TM_OBJECTIVE_CRITICAL_PATH;
 
-  // critical path needs every node's unrestricted top-2 (first occurrence).
-  if (objective == TM_OBJECTIVE_CRITICAL_PATH) {
-    for (int t = tid; t < T; t += kRouteThreads) {
-      const float* g = gates + (size_t)t * E;
+  if (critical) {
+    for (int t = tid; t < T; t += kThreads) {
+      const float* g = a.gates + (size_t)t * E;
       int u1 = 0;
       float b1 = g[0];
       for (int e = 1; e < E; ++e) {
@@ -123,23 +152,23 @@ tm_route_bucket_kernel(const float* __restrict__ gates, const float* __restrict_
         const float v = g[e];
         if (u2 < 0 || v > b2) { b2 = v; u2 = e; }
       }
-      s_fe[2 * t] = (uint8_t)u1;
-      s_fe[2 * t + 1] = (uint8_t)u2;
+      sh.fe[2 * t] = (uint8_t)u1;
+      sh.fe[2 * t + 1] = (uint8_t)u2;
     }
     __syncthreads();
   }
 
   // 1. demand (and criticality)
-  for (int e = wave; e < E; e += kRouteWaves) {
+  for (int e = wave; e < E; e += kWaves) {
     float acc = 0.0f;
     float crit = -INFINITY;
     for (int t = lane; t < T; t += 64) {
-      const float a = accept[t];
-      const float p = a * gates[(size_t)t * E + e];
+      const float av = a.accept[t];
+      const float p = av * a.gates[(size_t)t * E + e];
       acc = acc + p;
-      if (objective == TM_OBJECTIVE_CRITICAL_PATH) {
-        const bool needed = (s_fe[2 * t] == e) || ((s_fe[2 * t + 1] == e) && (a >= tau));
-        if (needed) crit = fmaxf(crit, a);
+      if (critical) {
+        const bool needed = (sh.fe[2 * t] == e) || ((sh.fe[2 * t + 1] == e) && (av >= a.tau));
+        if (needed) crit = fmaxf(crit, av);
       }
     }
 #pragma unroll
@@ -148,76 +177,73 @@ tm_route_bucket_kernel(const float* __restrict__ gates, const float* __restrict_
       crit = fmaxf(crit, __shfl_xor(crit, off));
     }
     if (lane == 0) {
-      s_demand[e] = acc;
-      s_crit[e] = crit;
-      demand_out[e] = acc;
+      sh.demand[e] = acc;
+      sh.crit[e] = crit;
+      a.demand_out[e] = acc;
     }
   }
+  // fill the padded layout while the keep set is chosen (scattered into below)
+  for (int i = tid; i < padded_rows; i += kThreads) a.padded_slots[i] = -1;
   __syncthreads();
 
   // 2. keep set: selection in lexicographic order, first occurrence on ties.
   if (tid == 0) {
-    for (int e = 0; e < E; ++e) s_keep[e] = 0;
-    for (int rank = 0; rank < budget; ++rank) {
+    for (int e = 0; e < E; ++e) sh.keep[e] = 0;
+    for (int rank = 0; rank < a.budget; ++rank) {
       int best = -1;
       for (int e = 0; e < E; ++e) {
-        if (s_keep[e]) continue;
+        if (sh.keep[e]) continue;
         if (best < 0) { best = e; continue; }
         bool better;
-        if (objective == TM_OBJECTIVE_CRITICAL_PATH) {
-          better = (s_crit[e] > s_crit[best]) ||
-                   (s_crit[e] == s_crit[best] && s_demand[e] > s_demand[best]);
+        if (critical) {
+          better = (sh.crit[e] > sh.crit[best]) ||
+                   (sh.crit[e] == sh.crit[best] && sh.demand[e] > sh.demand[best]);
         } else {
-          better = s_demand[e] > s_demand[best];
+          better = sh.demand[e] > sh.demand[best];
         }
         if (better) best = e;
       }
-      s_keep[best] = 1;
+      sh.keep[best] = 1;
     }
   }
   __syncthreads();
 
   // 3. in-budget top-2, renormalisation, low-acceptance degrade
-  for (int t = tid; t < T; t += kRouteThreads) {
-    const float* g = gates + (size_t)t * E;
+  for (int t = tid; t < T; t += kThreads) {
+    const float* g = a.gates + (size_t)t * E;
     int i1 = -1;
     float g1 = 0.0f;
     for (int e = 0; e < E; ++e) {
-      const float v = s_keep[e] ? g[e] : 0.0f;
+      const float v = sh.keep[e] ? g[e] : 0.0f;
       if (i1 < 0 || v > g1) { g1 = v; i1 = e; }
     }
     int i2 = -1;
     float g2 = 0.0f;
     for (int e = 0; e < E; ++e) {
       if (e == i1) continue;
-      const float v = s_keep[e] ? g[e] : 0.0f;
+      const float v = sh.keep[e] ? g[e] : 0.0f;
       if (i2 < 0 || v > g2) { g2 = v; i2 = e; }
     }
     const float s = g1 + g2;
     float tg1 = g1 / s;
     float tg2 = g2 / s;
-    if (accept[t] < tau) { tg1 = 1.0f; tg2 = 0.0f; }
-    topk_ids[2 * t] = i1;
-    topk_ids[2 * t + 1] = i2;
-    gates_flat[2 * t] = tg1;
-    gates_flat[2 * t + 1] = tg2;
+    if (a.accept[t] < a.tau) { tg1 = 1.0f; tg2 = 0.0f; }
+    a.topk_ids[2 * t] = i1;
+    a.topk_ids[2 * t + 1] = i2;
+    a.gates_flat[2 * t] = tg1;
+    a.gates_flat[2 * t + 1] = tg2;
+    sh.fe[2 * t] = (uint8_t)i1;  // the critical-path use of fe ended at the barrier above
+    sh.fe[2 * t + 1] = (uint8_t)i2;
   }
-  // s_fe may still be read by step 1 of slower waves: fence before rewriting it.
-  __syncthreads();
-  for (int t = tid; t < T; t += kRouteThreads) {
-    s_fe[2 * t] = (uint8_t)topk_ids[2 * t];
-    s_fe[2 * t + 1] = (uint8_t)topk_ids[2 * t + 1];
-  }
-  for (int i = tid; i < padded_rows; i += kRouteThreads) s_padded[i] = -1;
   __syncthreads();
 
   // 4a. per-chunk expert counts from ballots
-  for (int q = wave; q < nchunk; q += kRouteWaves) {
+  for (int q = wave; q < nchunk; q += kWaves) {
     const int s = q * 64 + lane;
-    const int fe = (s < nslot) ? (int)s_fe[s] : -1;
+    const int fe = (s < nslot) ? (int)sh.fe[s] : -1;
     for (int e = 0; e < E; ++e) {
       const unsigned long long m = __ballot(fe == e);
-      if (lane == 0) s_cnt[q * TM_MAX_EXPERTS + e] = (uint16_t)__popcll(m);
+      if (lane == 0) sh.cnt[q * TM_MAX_EXPERTS + e] = (uint16_t)__popcll(m);
     }
   }
   __syncthreads();
@@ -225,11 +251,11 @@ tm_route_bucket_kernel(const float* __restrict__ gates, const float* __restrict_
   if (tid < E) {
     int run = 0;
     for (int q = 0; q < nchunk; ++q) {
-      const int c = s_cnt[q * TM_MAX_EXPERTS + tid];
-      s_cnt[q * TM_MAX_EXPERTS + tid] = (uint16_t)run;
+      const int c = sh.cnt[q * TM_MAX_EXPERTS + tid];
+      sh.cnt[q * TM_MAX_EXPERTS + tid] = (uint16_t)run;
       run += c;
     }
-    s_count[tid] = run;
+    sh.count[tid] = run;
   }
   __syncthreads();
   // 4c. block layout (reference), compact offsets and GEMM tiles
@@ -238,61 +264,132 @@ tm_route_bucket_kernel(const float* __restrict__ gates, const float* __restrict_
     int off = 0;
     int j = 0;
     for (int e = 0; e < E; ++e) {
-      const int c = s_count[e];
-      const int nb = (c + BM - 1) / BM;
-      s_block_start[e] = blocks;
-      s_nblocks[e] = nb;
+      const int c = sh.count[e];
+      const int nb = (c + a.BM - 1) / a.BM;
+      sh.block_start[e] = blocks;
+      sh.nblocks[e] = nb;
       blocks += nb;
-      s_offset[e] = off;
+      sh.offset[e] = off;
       for (int r = 0; r < c; r += TM_GEMM_TILE_M) {
-        if (j < max_tiles) {
-          tiles[4 * j + 0] = e;
-          tiles[4 * j + 1] = off + r;
-          tiles[4 * j + 2] = min(TM_GEMM_TILE_M, c - r);
-          tiles[4 * j + 3] = 0;
+        if (j < a.max_tiles) {
+          a.tiles[4 * j + 0] = e;
+          a.tiles[4 * j + 1] = off + r;
+          a.tiles[4 * j + 2] = min(TM_GEMM_TILE_M, c - r);
+          a.tiles[4 * j + 3] = 0;
         }
         ++j;
       }
       off += c;
     }
-    s_offset[E] = off;
-    for (; j < max_tiles; ++j) {
-      tiles[4 * j + 0] = -1;
-      tiles[4 * j + 1] = 0;
-      tiles[4 * j + 2] = 0;
-      tiles[4 * j + 3] = 0;
+    sh.offset[E] = off;
+    for (; j < a.max_tiles; ++j) {
+      a.tiles[4 * j + 0] = -1;
+      a.tiles[4 * j + 1] = 0;
+      a.tiles[4 * j + 2] = 0;
+      a.tiles[4 * j + 3] = 0;
     }
   }
   __syncthreads();
-  if (tid <= E) expert_offsets[tid] = s_offset[tid];
+  if (tid <= E) a.expert_offsets[tid] = sh.offset[tid];
   // 4d. stable in-expert rank -> destinations
-  for (int q = wave; q < nchunk; q += kRouteWaves) {
+  for (int q = wave; q < nchunk; q += kWaves) {
     const int s = q * 64 + lane;
-    const int fe = (s < nslot) ? (int)s_fe[s] : -1;
+    const int fe = (s < nslot) ? (int)sh.fe[s] : -1;
     int inrank = 0;
     for (int e = 0; e < E; ++e) {
       const unsigned long long m = __ballot(fe == e);
       if (fe == e) inrank = __popcll(m & ((1ull << lane) - 1ull));
     }
     if (s < nslot) {
-      const int rank = (int)s_cnt[q * TM_MAX_EXPERTS + fe] + inrank;
-      const int dest = s_block_start[fe] * BM + rank;
-      const int pos = s_offset[fe] + rank;
-      slot_to_row[s] = dest;
-      if (dest < padded_rows) s_padded[dest] = (int16_t)s;
-      sorted_slots[pos] = s;
-      slot_pos[s] = pos;
+      const int rank = (int)sh.cnt[q * TM_MAX_EXPERTS + fe] + inrank;
+      const int dest = sh.block_start[fe] * a.BM + rank;
+      const int pos = sh.offset[fe] + rank;
+      a.slot_to_row[s] = dest;
+      if (dest < padded_rows) a.padded_slots[dest] = s;
+      a.sorted_slots[pos] = s;
+      a.slot_pos[s] = pos;
     }
   }
-  __syncthreads();
-  for (int i = tid; i < padded_rows; i += kRouteThreads) padded_slots[i] = s_padded[i];
-  for (int b = tid; b < max_blocks; b += kRouteThreads) {
+  for (int b = tid; b < a.max_blocks; b += kThreads) {
     int owner = -1;
     for (int e = 0; e < E; ++e) {
-      if (s_nblocks[e] > 0 && b >= s_block_start[e] && b < s_block_start[e] + s_nblocks[e]) owner = e;
+      if (sh.nblocks[e] > 0 && b >= sh.block_start[e] && b < sh.block_start[e] + sh.nblocks[e])
+        owner = e;
     }
-    block_expert_ids[b] = owner;
+    a.block_expert_ids[b] = owner;
   }
+}
+
+__global__ void __launch_bounds__(kThreads)
+tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
+                 float* __restrict__ gates, int T, int H, int E) {
+  __shared__ float s_logit[TM_MAX_EXPERTS];
+  router_token(x, wg, gates, blockIdx.x, H, E, s_logit);
+}
+
+__global__ void __launch_bounds__(kThreads) tm_bucket_kernel(BucketArgs args) {
+  __shared__ BucketShared sh;
+  bucket_all(args, sh);
+}
+
+// Router for token blockIdx.x, then the last workgroup to finish buckets all
+// tokens.  `counter` is zero on entry and is returned to zero by that
+// workgroup.
+__global__ void __launch_bounds__(kThreads)
+tm_route_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int H,
+                BucketArgs args, float* __restrict__ gates, uint32_t* __restrict__ counter) {
+  __shared__ float s_logit[TM_MAX_EXPERTS];
+  __shared__ BucketShared sh;
+  __shared__ int s_last;
+  router_token(x, wg, gates, blockIdx.x, H, args.E, s_logit);
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = (atomicAdd(counter, 1u) == gridDim.x - 1u);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  bucket_all(args, sh);
+  if (threadIdx.x == 0) *counter = 0u;
+}
+
+int check_bucket_args(int64_t T, int64_t E, int64_t budget, int objective, int64_t block_m,
+                      int64_t max_blocks, int64_t max_tiles) {
+  if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS) return TM_ERR_SHAPE;
+  if (budget < 2 || budget > E) return TM_ERR_ARG;
+  if (objective != TM_OBJECTIVE_MASS && objective != TM_OBJECTIVE_CRITICAL_PATH) return TM_ERR_ARG;
+  if (block_m != 16 && block_m != 32) return TM_ERR_ARG;
+  if (max_blocks < 1 || max_blocks * block_m > kMaxPaddedRows || max_tiles < 1) return TM_ERR_SHAPE;
+  return TM_OK;
+}
+
+BucketArgs make_args(const float* gates, const float* accept, int64_t T, int64_t E,
+                     int64_t budget, float tau, int objective, int64_t block_m,
+                     int64_t max_blocks, int64_t max_tiles, int64_t* topk_ids,
+                     float* gates_flat, int64_t* padded_slots, int64_t* block_expert_ids,
+                     int64_t* slot_to_row, float* demand, int32_t* expert_offsets,
+                     int32_t* sorted_slots, int32_t* slot_pos, int32_t* tiles) {
+  BucketArgs a;
+  a.gates = gates;
+  a.accept = accept;
+  a.T = (int)T;
+  a.E = (int)E;
+  a.budget = (int)budget;
+  a.objective = objective;
+  a.BM = (int)block_m;
+  a.max_blocks = (int)max_blocks;
+  a.max_tiles = (int)max_tiles;
+  a.tau = tau;
+  a.topk_ids = topk_ids;
+  a.gates_flat = gates_flat;
+  a.padded_slots = padded_slots;
+  a.block_expert_ids = block_expert_ids;
+  a.slot_to_row = slot_to_row;
+  a.demand_out = demand;
+  a.expert_offsets = expert_offsets;
+  a.sorted_slots = sorted_slots;
+  a.slot_pos = slot_pos;
+  a.tiles = tiles;
+  return a;
 }
 
 }  // namespace
@@ -302,9 +399,9 @@ extern "C" int tm_op1_router_gates(const void* x, const void* wg, int64_t T, int
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS || H < 8 || (H % 8) != 0)
     return TM_ERR_SHAPE;
   if (((uintptr_t)x % 16) != 0 || ((uintptr_t)wg % 16) != 0) return TM_ERR_ALIGN;
-  const dim3 grid((unsigned)((T + 3) / 4));
-  hipLaunchKernelGGL(tm_router_kernel, grid, dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E);
+  hipLaunchKernelGGL(tm_router_kernel, dim3((unsigned)T), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)wg, gates, (int)T,
+                     (int)H, (int)E);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
@@ -317,16 +414,36 @@ extern "C" int tm_op1_route_bucket(const float* gates, const float* accept, int6
                                    int64_t* slot_to_row, float* demand,
                                    int32_t* expert_offsets, int32_t* sorted_slots,
                                    int32_t* slot_pos, int32_t* tiles, void* stream) {
-  if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS) return TM_ERR_SHAPE;
-  if (budget < 2 || budget > E) return TM_ERR_ARG;
-  if (objective != TM_OBJECTIVE_MASS && objective != TM_OBJECTIVE_CRITICAL_PATH) return TM_ERR_ARG;
-  if (block_m != 16 && block_m != 32) return TM_ERR_ARG;
-  if (max_blocks < 1 || max_blocks * block_m > kMaxPaddedRows || max_tiles < 1) return TM_ERR_SHAPE;
-  hipLaunchKernelGGL(tm_route_bucket_kernel, dim3(1), dim3(kRouteThreads), 0,
-                     (hipStream_t)stream, gates, accept, (int)T, (int)E, (int)budget, tau,
-                     objective, (int)block_m, (int)max_blocks, (int)max_tiles, topk_ids,
-                     gates_flat, padded_slots, block_expert_ids, slot_to_row, demand,
-                     expert_offsets, sorted_slots, slot_pos, tiles);
+  const int rc = check_bucket_args(T, E, budget, objective, block_m, max_blocks, max_tiles);
+  if (rc != TM_OK) return rc;
+  const BucketArgs a = make_args(gates, accept, T, E, budget, tau, objective, block_m, max_blocks,
+                                 max_tiles, topk_ids, gates_flat, padded_slots,
+                                 block_expert_ids, slot_to_row, demand, expert_offsets,
+                                 sorted_slots, slot_pos, tiles);
+  hipLaunchKernelGGL(tm_bucket_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, a);
+  TM_HIP_CHECK_LAUNCH();
+  return TM_OK;
+}
+
+extern "C" int tm_op1_route(const void* x, const void* wg, const float* accept, int64_t T,
+                            int64_t H, int64_t E, int64_t budget, float tau, int objective,
+                            int64_t block_m, int64_t max_blocks, int64_t max_tiles,
+                            float* gates, int64_t* topk_ids, float* gates_flat,
+                            int64_t* padded_slots, int64_t* block_expert_ids,
+                            int64_t* slot_to_row, float* demand, int32_t* expert_offsets,
+                            int32_t* sorted_slots, int32_t* slot_pos, int32_t* tiles,
+                            uint32_t* counter, void* stream) {
+  const int rc = check_bucket_args(T, E, budget, objective, block_m, max_blocks, max_tiles);
+  if (rc != TM_OK) return rc;
+  if (H < 8 || (H % 8) != 0) return TM_ERR_SHAPE;
+  if (((uintptr_t)x % 16) != 0 || ((uintptr_t)wg % 16) != 0) return TM_ERR_ALIGN;
+  const BucketArgs a = make_args(gates, accept, T, E, budget, tau, objective, block_m, max_blocks,
+                                 max_tiles, topk_ids, gates_flat, padded_slots,
+                                 block_expert_ids, slot_to_row, demand, expert_offsets,
+                                 sorted_slots, slot_pos, tiles);
+  hipLaunchKernelGGL(tm_route_kernel, dim3((unsigned)T), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)wg, (int)H, a,
+                     gates, counter);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }

@@ -5,8 +5,8 @@ Same Python surface as the reference module treemoe/kernels/op1_tree_moe.py
 :81, ``Routing`` :568, ``route_experts`` :641, ``tree_moe_forward`` :711); the
 work runs in libtreemoe_amd.so:
 
-  router       tm_op1_router_gates   bf16 logits, fp32 softmax
-  routing      tm_op1_route_bucket   budget routing + bucketing, one workgroup
+  routing      tm_op1_route          router (bf16 logits, fp32 softmax) + budget
+                                     routing + bucketing, one launch
   gate/up      tm_op1_gemm1          MFMA, SwiGLU fused, h kept in bf16
   down         tm_op1_gemm2          MFMA, deterministic K split, gate applied
   combine      tm_op1_combine        fixed order, bf16 output
@@ -97,6 +97,7 @@ class _Workspace:
         self.sorted_slots = torch.zeros(2 * n, dtype=i32, device=device)
         self.slot_pos = torch.zeros(2 * n, dtype=i32, device=device)
         self.tiles = torch.zeros(self.max_tiles, 4, dtype=i32, device=device)
+        self.counter = torch.zeros(1, dtype=i32, device=device)
 
 
 _ws_cache: dict[tuple, _Workspace] = {}
@@ -123,6 +124,28 @@ def _launch_route_bucket(gates, accept, n, e, budget, tau, objective, block_m, m
          TM_OBJECTIVE[objective], block_m, max_blocks, max_tiles, ptr(topk),
          ptr(gates_flat), ptr(padded), ptr(blk), ptr(s2r), ptr(demand), ptr(offsets),
          ptr(sorted_slots), ptr(slot_pos), ptr(tiles), _capi.stream_of(device))
+
+
+def _launch_route(x, router_weight, accept, budget, tau, objective, block_m, max_blocks,
+                  max_tiles, gates, topk, gates_flat, padded, blk, s2r, demand, offsets,
+                  sorted_slots, slot_pos, tiles, counter) -> None:
+    n, hidden = x.shape
+    call("tm_op1_route", ptr(x), ptr(router_weight), ptr(accept), n, hidden,
+         router_weight.shape[0], budget, float(tau), TM_OBJECTIVE[objective], block_m,
+         max_blocks, max_tiles, ptr(gates), ptr(topk), ptr(gates_flat), ptr(padded), ptr(blk),
+         ptr(s2r), ptr(demand), ptr(offsets), ptr(sorted_slots), ptr(slot_pos), ptr(tiles),
+         ptr(counter), _capi.stream_of(x.device))
+
+
+_counters: dict[int, torch.Tensor] = {}
+
+
+def _counter(device: torch.device) -> torch.Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    c = _counters.get(idx)
+    if c is None:
+        c = _counters[idx] = torch.zeros(1, dtype=torch.int32, device=device)
+    return c
 
 
 def _prep_accept(node_accept_prob: torch.Tensor, n: int) -> torch.Tensor:
@@ -155,13 +178,6 @@ def route_and_bucket(
     if block_m not in (16, 32):
         raise ValueError("block_m must be 16 or 32")
     dev = x.device
-    if router_gates is None:
-        _require_bf16("x", x)
-        _require_bf16("router_weight", router_weight)
-        gates = torch.empty(n, e, dtype=torch.float32, device=dev)
-        _launch_router(x, router_weight, gates)
-    else:
-        gates = router_gates.float().contiguous()
     accept = _prep_accept(node_accept_prob, n)
     max_blocks = compact_block_capacity(2 * n, expert_budget, block_m)
     max_tiles = compact_block_limit(2 * n, expert_budget, TILE_M)
@@ -176,9 +192,20 @@ def route_and_bucket(
     sorted_slots = torch.empty(2 * n, dtype=i32, device=dev)
     slot_pos = torch.empty(2 * n, dtype=i32, device=dev)
     tiles = torch.empty(max_tiles, 4, dtype=i32, device=dev)
-    _launch_route_bucket(gates, accept, n, e, expert_budget, top1_threshold,
-                         routing_objective, block_m, max_blocks, max_tiles, topk, gflat,
-                         padded, blk, s2r, demand, offsets, sorted_slots, slot_pos, tiles, dev)
+    if router_gates is None:
+        _require_bf16("x", x)
+        _require_bf16("router_weight", router_weight)
+        gates = torch.empty(n, e, dtype=torch.float32, device=dev)
+        _launch_route(x, router_weight, accept, expert_budget, top1_threshold,
+                      routing_objective, block_m, max_blocks, max_tiles, gates, topk, gflat,
+                      padded, blk, s2r, demand, offsets, sorted_slots, slot_pos, tiles,
+                      _counter(dev))
+    else:
+        gates = router_gates.float().contiguous()
+        _launch_route_bucket(gates, accept, n, e, expert_budget, top1_threshold,
+                             routing_objective, block_m, max_blocks, max_tiles, topk, gflat,
+                             padded, blk, s2r, demand, offsets, sorted_slots, slot_pos, tiles,
+                             dev)
     result = (topk.view(n, 2), gflat.view(n, 2), padded, blk, s2r, max_blocks)
     if return_demand:
         return (*result, demand)
@@ -279,14 +306,13 @@ def route_experts(
     max_blocks = compact_block_capacity(2 * n, expert_budget, BM)
     launch_blocks = compact_block_limit(2 * n, expert_budget, BM)
     max_tiles = compact_block_limit(2 * n, expert_budget, TILE_M)
-    _launch_router(x, router_weight, ws.router_gates)
     padded = ws.padded_slots[: max_blocks * BM]
     blk = ws.block_expert_ids[:max_blocks]
     tiles = ws.tiles[:max_tiles]
-    _launch_route_bucket(ws.router_gates, accept, n, e, expert_budget, top1_threshold,
-                         routing_objective, BM, max_blocks, max_tiles, ws.topk_flat,
-                         ws.gates_flat, padded, blk, ws.slot_to_row, ws.demand,
-                         ws.expert_offsets, ws.sorted_slots, ws.slot_pos, tiles, x.device)
+    _launch_route(x, router_weight, accept, expert_budget, top1_threshold, routing_objective,
+                  BM, max_blocks, max_tiles, ws.router_gates, ws.topk_flat, ws.gates_flat,
+                  padded, blk, ws.slot_to_row, ws.demand, ws.expert_offsets, ws.sorted_slots,
+                  ws.slot_pos, tiles, ws.counter)
     return Routing(ws, ws.router_gates, ws.topk_flat.view(n, 2), ws.gates_flat, padded, blk,
                    ws.slot_to_row, max_blocks, launch_blocks, ws.demand, ws.expert_offsets,
                    ws.sorted_slots, ws.slot_pos, tiles, max_tiles)
