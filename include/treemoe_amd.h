@@ -117,8 +117,11 @@ int tm_op1_route(const void* x, const void* wg, const float* accept, int64_t T,
  * Replaces `_moe_gemm1_kernel` (treemoe/kernels/op1_tree_moe.py:300-383):
  *   h[p, :] = bf16( silu(x[tok] . w1[e]^T) * (x[tok] . w3[e]^T) ), fp32 accumulate,
  * for sorted row p of expert e, tok = sorted_slots[p] / 2.
- * x: [T, H] bf16, w1/w3: [E, I, H] bf16, h: [2T, I] bf16 (workspace).
- * Requires H % 256 == 0 and I % 64 == 0.
+ * x: [T, H] bf16, w1/w3: [E, I, H] bf16.  h is a workspace of
+ * max_tiles * TM_GEMM_TILE_M * I bf16 elements holding each tile's rows in
+ * MFMA A-fragment order (tile j, 16-row sub-tile b, 32-column k-step s: 64
+ * lanes x 8 elements, lane = (k/8 % 4) * 16 + row % 16), the layout
+ * tm_op1_gemm2 consumes.  Requires H % 256 == 0 and I % 256 == 0.
  */
 int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void* h,
                  const int32_t* sorted_slots, const int32_t* tiles,
@@ -129,8 +132,9 @@ int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void* h,
  * Down projection, split over K = I into `split` deterministic segments.
  * Replaces `_moe_gemm2_det_kernel` (treemoe/kernels/op1_tree_moe.py:447-509):
  *   y[s, p, :] = gates_flat[slot] * ( h[p, Ks] . w2[e][:, Ks]^T ), fp32,
- * h: [2T, I] bf16, w2: [E, H, I] bf16, y: [split, 2T, H] fp32 (workspace).
- * Requires H % 64 == 0 and (I / split) % 256 == 0.
+ * h: the tile-swizzled workspace written by tm_op1_gemm1, w2: [E, H, I] bf16,
+ * y: [split, 2T, H] fp32 (workspace).
+ * Requires H % 32 == 0 and (I / split) % 256 == 0.
  */
 int tm_op1_gemm2(const void* h, const void* w2, float* y,
                  const float* gates_flat, const int32_t* sorted_slots,

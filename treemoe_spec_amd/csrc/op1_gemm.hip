@@ -1,41 +1,50 @@
 // op1 expert GEMMs on gfx950: gate/up + SwiGLU, down projection with a
 // deterministic K split, and the fixed-order combine.
 //
-// Work unit = (GEMM tile of <= 64 sorted rows of one expert) x (64 weight rows).
-// A workgroup is 4 waves; wave w owns 16 weight rows and all 16-row sub-tiles
-// of the tile (NSUB = 1..4, a template parameter chosen per tile), so every
-// weight byte is read from HBM once per tile.  Weights go global -> VGPR with
-// 16-byte non-temporal buffer loads laid out as the B operand of
-// v_mfma_f32_16x16x32_bf16 (lane l: weight row l%16, k-group l/16), one
-// 256-element K chunk ahead of the MFMAs.  Activation rows (x gathered by
-// token, or h) are staged through a double-buffered LDS tile; a chunk's
-// activation loads are issued before its weight loads, so storing them to LDS
-// waits only for older loads and the next chunk's weights stay in flight
-// across the workgroup barrier.  The loop has no data-dependent branches: the
-// prefetch past the last chunk uses an out-of-range buffer offset, which
-// returns zeros without touching memory.
+// Work item = one workgroup = 2 x 16 weight rows of one expert (the same rows of
+// w1 and w3, or two adjacent row blocks of w2) x one GEMM tile
+// (<= 64 sorted rows of that expert, NSUB = ceil(rows/16) 16-row sub-tiles,
+// a template parameter chosen per tile).  The 4 waves of the workgroup split
+// the reduction dimension: wave w takes K chunks w, w+4, w+8, ...; their
+// partial sums are added in LDS in the fixed order (wave 0 + 1 + 2 + 3), so
+// results are bitwise reproducible.  Small items keep the drain at the end of
+// each launch short.
+//
+// Weights stream HBM -> VGPR with coalesced 16-byte non-temporal buffer loads
+// (one instruction = 8 rows x 128 contiguous bytes), one chunk ahead of use,
+// and are turned into v_mfma_f32_16x16x32_bf16 B operands (lane l: row l%16,
+// k-group l/16) through a per-wave LDS scratch whose rows are padded by 16
+// bytes (conflict-free fragment reads).  Activations are read straight into A
+// operands: x rows gathered by token for the gate/up GEMM; for the down GEMM,
+// h, which the gate/up GEMM writes in A-fragment order ("swizzled": one 16-row
+// sub-tile x 32-column k-step = 64 lanes x 16 contiguous bytes), so every h
+// load is one contiguous 1 KB per wave.
 #include "tm_common.h"
 
 namespace {
 
-constexpr int KC = 256;            // K elements per staged chunk
-constexpr int LDS_LD = KC + 8;     // padded LDS row, elements (528 B, 16 B aligned)
-constexpr int NSTEP = KC / 32;     // MFMA k-steps per chunk
-constexpr int MT = TM_GEMM_TILE_M; // rows per tile
-constexpr int NWAVE = 4;
-constexpr int BN = 16 * NWAVE;     // weight rows per workgroup
+constexpr int WAVES = 4;
+constexpr int ROWS = 16;           // weight rows per workgroup
+constexpr int MT = TM_GEMM_TILE_M; // rows per GEMM tile (<= 4 sub-tiles)
 constexpr uint32_t kOutOfRange = 0x80000000u;
 constexpr int kNt = 2;             // buffer cache policy: non-temporal
+constexpr int kScratchBytes = 69632;  // >= 4 waves x 2 matrices x 16 rows x 528 B
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+template <int NSUB>
+struct Cfg {
+  static constexpr int KC = NSUB <= 1 ? 256 : (NSUB == 2 ? 128 : 64);  // K elements per chunk
+  static constexpr int NSTEP = KC / 32;             // MFMA k-steps per chunk
+  static constexpr int WLD = KC / 32;               // 1 KB weight loads per matrix per chunk
+  static constexpr int SROW = KC * 2 + 16;          // scratch row stride, bytes
+};
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t tm_buffer(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
 
-// Operands travel as 32-bit integer vectors and become bf16x8 only at the MFMA
-// (bf16 vectors built from integer loads would be repacked element-wise).
 template <int AUX>
 __device__ __forceinline__ u32x4_t ld_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
@@ -46,75 +55,92 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// Activation tile rows staged for NSUB sub-tiles: thread tid stages pieces
-// p = tid + 256*i (i < 2*NSUB): tile row (tid >> 5) + 8*i, columns
-// (tid & 31)*8 .. +8.  off[i] is the byte offset of that row segment at k = 0,
-// or kOutOfRange for rows past the tile (zeros).
-template <int NSUB>
-struct Acts {
-  static constexpr int XP = 2 * NSUB;
-  __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t off[XP];
-  int lds_off;  // element offset of this thread's first piece in a stage
-
-  __device__ __forceinline__ void load(u32x4_t (&v)[XP], uint32_t kbyte, bool valid) const {
-#pragma unroll
-    for (int i = 0; i < XP; ++i) v[i] = ld_b128<0>(rsrc, valid ? off[i] + kbyte : kOutOfRange);
-  }
-  __device__ __forceinline__ void store(uint16_t* stage, const u32x4_t (&v)[XP]) const {
-#pragma unroll
-    for (int i = 0; i < XP; ++i)
-      *reinterpret_cast<u32x4_t*>(stage + lds_off + 8 * i * LDS_LD) = v[i];
-  }
-};
-
-// Weight rows of one matrix for this lane: row n (within the expert), k-group g.
-struct Weights {
-  __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t off;  // byte offset of (n, 8g) at the first chunk
-
-  __device__ __forceinline__ void load(u32x4_t (&w)[NSTEP], uint32_t kbyte, bool valid) const {
-#pragma unroll
-    for (int s = 0; s < NSTEP; ++s)
-      w[s] = ld_b128<kNt>(rsrc, valid ? off + kbyte + 64u * s : kOutOfRange);
-  }
-};
-
 // Keep the machine scheduler from sinking the next chunk's loads below the
-// current chunk's MFMAs (which would shrink the bytes in flight to a few KB).
+// current chunk's MFMAs.
 __device__ __forceinline__ void tm_sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-__device__ __forceinline__ u32x4_t lds_frag(const uint16_t* stage, int row, int s, int g) {
-  return *reinterpret_cast<const u32x4_t*>(stage + row * LDS_LD + s * 32 + g * 8);
+// 16 weight rows of one matrix, coalesced: load q (0 <= q < WLD) covers rows
+// 8*(q&1) + lane/8 and bytes 128*(q>>1) + 16*(lane%8) of the chunk.
+template <int NSUB>
+struct WeightRows {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t base;     // byte offset of (first row + lane/8, 16*(lane%8)) at k = 0
+  uint32_t half;     // byte distance of 8 rows
+  int lds_w;         // scratch byte offset written by this lane for q = 0
+
+  __device__ __forceinline__ void load(u32x4_t (&v)[Cfg<NSUB>::WLD], uint32_t kbyte,
+                                       bool valid) const {
+#pragma unroll
+    for (int q = 0; q < Cfg<NSUB>::WLD; ++q) {
+      const uint32_t off = base + kbyte + (q & 1) * half + (q >> 1) * 128u;
+      v[q] = ld_b128<kNt>(rsrc, valid ? off : kOutOfRange);
+    }
+  }
+  __device__ __forceinline__ void stage(uint8_t* scratch,
+                                        const u32x4_t (&v)[Cfg<NSUB>::WLD]) const {
+#pragma unroll
+    for (int q = 0; q < Cfg<NSUB>::WLD; ++q)
+      *reinterpret_cast<u32x4_t*>(scratch + lds_w + (q & 1) * 8 * Cfg<NSUB>::SROW + (q >> 1) * 128) =
+          v[q];
+  }
+};
+
+// B fragment of k-step s from the scratch: lane l reads row l%16, k-group l/16.
+template <int NSUB>
+__device__ __forceinline__ u32x4_t b_frag(const uint8_t* scratch, int lane, int s) {
+  return *reinterpret_cast<const u32x4_t*>(scratch + (lane & 15) * Cfg<NSUB>::SROW + s * 64 +
+                                           (lane >> 4) * 16);
+}
+
+// Fixed-order sum of the 4 waves' partial accumulators (wave 0 + 1 + 2 + 3)
+// through LDS; returns the total for sub-tile `sub` of matrix `mat` in the
+// wave that calls it (one wave per sub-tile).
+__device__ __forceinline__ f32x4_t reduce_partials(const f32x4_t* red, int nsub, int sub, int mat,
+                                                   int nmat, int lane) {
+  f32x4_t s = red[((0 * nsub + sub) * nmat + mat) * 64 + lane];
+#pragma unroll
+  for (int w = 1; w < WAVES; ++w) {
+    const f32x4_t p = red[((w * nsub + sub) * nmat + mat) * 64 + lane];
+    s[0] = s[0] + p[0];
+    s[1] = s[1] + p[1];
+    s[2] = s[2] + p[2];
+    s[3] = s[3] + p[3];
+  }
+  return s;
 }
 
 // ----------------------------------------------------------------- GEMM1 --
 // h[p, n] = bf16( silu(sum_k x[tok(p), k] w1[e, n, k]) * sum_k x[tok(p), k] w3[e, n, k] )
 template <int NSUB>
-__device__ __forceinline__ void gemm1_body(uint16_t* __restrict__ lds, const uint16_t* x,
-                                           const uint16_t* w1, const uint16_t* w3,
-                                           uint16_t* __restrict__ h,
-                                           const int32_t* __restrict__ sorted_slots, int e,
-                                           int row0, int rows, int H, int I, uint32_t x_bytes) {
+__device__ __forceinline__ void gemm1_item(uint8_t* lds, const uint16_t* x, const uint16_t* w1,
+                                           const uint16_t* w3, uint16_t* __restrict__ hsw,
+                                           const int32_t* __restrict__ sorted_slots, int tile,
+                                           int e, int row0, int rows, int H, int I,
+                                           uint32_t x_bytes) {
+  using C = Cfg<NSUB>;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int r = lane & 15, g = lane >> 4;
-  const int n = blockIdx.x * BN + wave * 16 + r;
-  const size_t ebase = (size_t)e * I * H;
+  const int ng = blockIdx.x;
+  uint8_t* scratch = lds + wave * 2 * ROWS * C::SROW;
 
-  Acts<NSUB> act;
-  act.rsrc = tm_buffer(x, x_bytes);
-  act.lds_off = (tid >> 5) * LDS_LD + (tid & 31) * 8;
+  WeightRows<NSUB> wr1, wr3;
+  const size_t ebase = (size_t)e * I * H;
+  wr1.rsrc = tm_buffer(w1 + ebase, (uint32_t)((size_t)I * H * 2));
+  wr3.rsrc = tm_buffer(w3 + ebase, (uint32_t)((size_t)I * H * 2));
+  wr1.base = wr3.base = (uint32_t)(ng * ROWS + (lane >> 3)) * (uint32_t)H * 2u + (lane & 7) * 16u;
+  wr1.half = wr3.half = 8u * (uint32_t)H * 2u;
+  wr1.lds_w = (lane >> 3) * C::SROW + (lane & 7) * 16;
+  wr3.lds_w = wr1.lds_w + ROWS * C::SROW;
+
+  const __amdgpu_buffer_rsrc_t xr = tm_buffer(x, x_bytes);
+  uint32_t xrow[NSUB];
 #pragma unroll
-  for (int i = 0; i < Acts<NSUB>::XP; ++i) {
-    const int m = (tid >> 5) + 8 * i;
-    act.off[i] = (m < rows) ? 2u * (uint32_t)((sorted_slots[row0 + m] >> 1) * H + (tid & 31) * 8)
-                            : kOutOfRange;
+  for (int sub = 0; sub < NSUB; ++sub) {
+    const int m = sub * 16 + (lane & 15);
+    xrow[sub] = (m < rows)
+                    ? 2u * (uint32_t)((sorted_slots[row0 + m] >> 1) * H + (lane >> 4) * 8)
+                    : kOutOfRange;
   }
-  Weights wt1, wt3;
-  wt1.rsrc = tm_buffer(w1 + ebase, (uint32_t)((size_t)I * H * 2));
-  wt3.rsrc = tm_buffer(w3 + ebase, (uint32_t)((size_t)I * H * 2));
-  wt1.off = wt3.off = 2u * (uint32_t)(n * H + g * 8);
 
   f32x4_t acc1[NSUB], acc3[NSUB];
 #pragma unroll
@@ -122,62 +148,77 @@ __device__ __forceinline__ void gemm1_body(uint16_t* __restrict__ lds, const uin
     acc1[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     acc3[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  u32x4_t a1[NSTEP], a3[NSTEP], b1[NSTEP], b3[NSTEP];
-  u32x4_t xr[Acts<NSUB>::XP];
-  uint16_t* L0 = lds;
-  uint16_t* L1 = lds + MT * LDS_LD;
+  u32x4_t a1[C::WLD], a3[C::WLD], b1[C::WLD], b3[C::WLD];
+  u32x4_t ax[C::NSTEP * NSUB], bx[C::NSTEP * NSUB];
 
-  auto compute = [&](const uint16_t* stage, const u32x4_t (&w1r)[NSTEP],
-                     const u32x4_t (&w3r)[NSTEP]) {
+  auto load = [&](u32x4_t (&w1r)[C::WLD], u32x4_t (&w3r)[C::WLD],
+                  u32x4_t (&xf)[C::NSTEP * NSUB], int c, bool valid) {
+    const uint32_t kb = (uint32_t)c * C::KC * 2u;
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
+    for (int s = 0; s < C::NSTEP; ++s)
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub)
+        xf[s * NSUB + sub] = ld_b128<0>(xr, valid ? xrow[sub] + kb + s * 64u : kOutOfRange);
+    wr1.load(w1r, kb, valid);
+    wr3.load(w3r, kb, valid);
+  };
+  auto process = [&](const u32x4_t (&w1r)[C::WLD], const u32x4_t (&w3r)[C::WLD],
+                     const u32x4_t (&xf)[C::NSTEP * NSUB]) {
+    wr1.stage(scratch, w1r);
+    wr3.stage(scratch, w3r);
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) {
+      const u32x4_t f1 = b_frag<NSUB>(scratch, lane, s);
+      const u32x4_t f3 = b_frag<NSUB>(scratch + ROWS * C::SROW, lane, s);
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
-        const u32x4_t a = lds_frag(stage, sub * 16 + r, s, g);
-        acc1[sub] = mfma16(a, w1r[s], acc1[sub]);
-        acc3[sub] = mfma16(a, w3r[s], acc3[sub]);
+        acc1[sub] = mfma16(xf[s * NSUB + sub], f1, acc1[sub]);
+        acc3[sub] = mfma16(xf[s * NSUB + sub], f3, acc3[sub]);
       }
     }
   };
 
-  const int nch = H / KC;
-  act.load(xr, 0, true);
-  wt1.load(a1, 0, true);
-  wt3.load(a3, 0, true);
-  act.store(L0, xr);
-  tm_lds_barrier();
-  for (int c = 0; c + 1 < nch; c += 2) {
-    const uint32_t k1 = (uint32_t)(c + 1) * KC * 2;
-    act.load(xr, k1, true);
-    wt1.load(b1, k1, true);
-    wt3.load(b3, k1, true);
+  const int nch = H / C::KC;
+  load(a1, a3, ax, wave, wave < nch);
+  // One basic block per trip (no early exit), so no load is sunk below the
+  // MFMAs it should overlap.  A chunk past the end loads zeros out of range
+  // and its MFMAs add exact zeros.
+  for (int c = wave; c < nch; c += 2 * WAVES) {
+    const int c1 = c + WAVES;
+    load(b1, b3, bx, c1, c1 < nch);
     tm_sched_fence();
-    compute(L0, a1, a3);
-    act.store(L1, xr);
-    tm_lds_barrier();
-    const bool more = (c + 2) < nch;
-    const uint32_t k2 = (uint32_t)(c + 2) * KC * 2;
-    act.load(xr, k2, more);
-    wt1.load(a1, k2, more);
-    wt3.load(a3, k2, more);
+    process(a1, a3, ax);
+    const int c2 = c1 + WAVES;
+    load(a1, a3, ax, c2, c2 < nch);
     tm_sched_fence();
-    compute(L1, b1, b3);
-    act.store(L0, xr);
-    tm_lds_barrier();
+    process(b1, b3, bx);
   }
-  if (nch & 1) compute(L0, a1, a3);
 
-  // epilogue: lane holds C[m = 4g + i][n] of each sub-tile
+  // cross-wave reduction in the (now free) scratch, then the SwiGLU epilogue
+  __syncthreads();
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(lds);
 #pragma unroll
   for (int sub = 0; sub < NSUB; ++sub) {
+    red[((wave * NSUB + sub) * 2 + 0) * 64 + lane] = acc1[sub];
+    red[((wave * NSUB + sub) * 2 + 1) * 64 + lane] = acc3[sub];
+  }
+  __syncthreads();
+  if (wave < NSUB) {
+    const int sub = wave;
+    const f32x4_t s1 = reduce_partials(red, NSUB, sub, 0, 2, lane);
+    const f32x4_t s3 = reduce_partials(red, NSUB, sub, 1, 2, lane);
+    const int r = lane & 15, g = lane >> 4;
+    const int n = ng * ROWS + r;
+    const int kk = n & 31;
+    const size_t frag = ((size_t)(tile * 4 + sub) * (I / 32) + (n >> 5)) * 64;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int m = sub * 16 + g * 4 + i;
-      if (m < rows) {
-        const float a = acc1[sub][i];
-        const float b = acc3[sub][i];
+      const int mm = g * 4 + i;  // row within the sub-tile
+      if (sub * 16 + mm < rows) {
+        const float a = s1[i];
+        const float b = s3[i];
         const float hv = (a / (1.0f + __expf(-a))) * b;
-        h[(size_t)(row0 + m) * I + n] = tm_f32_to_bf16(hv);
+        hsw[(frag + (kk >> 3) * 16 + mm) * 8 + (kk & 7)] = tm_f32_to_bf16(hv);
       }
     }
   }
@@ -185,125 +226,157 @@ __device__ __forceinline__ void gemm1_body(uint16_t* __restrict__ lds, const uin
 
 __global__ void __launch_bounds__(256, 2)
 tm_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
-                const uint16_t* __restrict__ w3, uint16_t* __restrict__ h,
+                const uint16_t* __restrict__ w3, uint16_t* __restrict__ hsw,
                 const int32_t* __restrict__ sorted_slots, const int32_t* __restrict__ tiles,
                 int H, int I, uint32_t x_bytes) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * MT * LDS_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kScratchBytes];
   const int tile = blockIdx.y;
   const int e = tiles[4 * tile];
   if (e < 0) return;
   const int row0 = tiles[4 * tile + 1];
   const int rows = tiles[4 * tile + 2];
   switch ((rows + 15) >> 4) {
-    case 1: gemm1_body<1>(lds, x, w1, w3, h, sorted_slots, e, row0, rows, H, I, x_bytes); break;
-    case 2: gemm1_body<2>(lds, x, w1, w3, h, sorted_slots, e, row0, rows, H, I, x_bytes); break;
-    case 3: gemm1_body<3>(lds, x, w1, w3, h, sorted_slots, e, row0, rows, H, I, x_bytes); break;
-    default: gemm1_body<4>(lds, x, w1, w3, h, sorted_slots, e, row0, rows, H, I, x_bytes); break;
+    case 1: gemm1_item<1>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
+    case 2: gemm1_item<2>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
+    case 3: gemm1_item<3>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
+    default: gemm1_item<4>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
   }
 }
 
 // ----------------------------------------------------------------- GEMM2 --
 // y[s, p, n] = gates_flat[slot(p)] * sum_{k in segment s} h[p, k] w2[e, n, k]
+// A workgroup streams two 16-row blocks of w2 (32 output columns) that share
+// the h fragments, so each wave keeps as many weight bytes in flight as in
+// the gate/up GEMM.
 template <int NSUB>
-__device__ __forceinline__ void gemm2_body(uint16_t* __restrict__ lds, const uint16_t* h,
-                                           const uint16_t* w2, float* __restrict__ y,
+__device__ __forceinline__ void gemm2_item(uint8_t* lds, const uint16_t* hsw, const uint16_t* w2,
+                                           float* __restrict__ y,
                                            const float* __restrict__ gates_flat,
-                                           const int32_t* __restrict__ sorted_slots, int e,
-                                           int row0, int rows, int R, int H, int I, int klen,
-                                           uint32_t h_bytes) {
+                                           const int32_t* __restrict__ sorted_slots, int tile,
+                                           int e, int row0, int rows, int R, int H, int I,
+                                           int klen, uint32_t h_bytes) {
+  using C = Cfg<NSUB>;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int r = lane & 15, g = lane >> 4;
-  const int n = blockIdx.x * BN + wave * 16 + r;
+  const int ng = blockIdx.x;  // 32 output columns
   const int split = blockIdx.y;
   const int kbase = split * klen;
+  uint8_t* scratch = lds + wave * 2 * ROWS * C::SROW;
 
-  Acts<NSUB> act;
-  act.rsrc = tm_buffer(h, h_bytes);
-  act.lds_off = (tid >> 5) * LDS_LD + (tid & 31) * 8;
+  WeightRows<NSUB> wr0, wr1;
+  wr0.rsrc = wr1.rsrc = tm_buffer(w2 + (size_t)e * H * I, (uint32_t)((size_t)H * I * 2));
+  wr0.base = (uint32_t)(ng * 2 * ROWS + (lane >> 3)) * (uint32_t)I * 2u + (uint32_t)kbase * 2u +
+             (lane & 7) * 16u;
+  wr1.base = wr0.base + (uint32_t)ROWS * (uint32_t)I * 2u;
+  wr0.half = wr1.half = 8u * (uint32_t)I * 2u;
+  wr0.lds_w = (lane >> 3) * C::SROW + (lane & 7) * 16;
+  wr1.lds_w = wr0.lds_w + ROWS * C::SROW;
+
+  // h fragments: sub-tile `sub`, global k-step ks -> 64 lanes x 16 contiguous bytes
+  const __amdgpu_buffer_rsrc_t hr = tm_buffer(hsw, h_bytes);
+  const uint32_t ksteps = (uint32_t)I / 32u;
+  const uint32_t hbase = ((uint32_t)tile * 4u * ksteps + (uint32_t)kbase / 32u) * 1024u + lane * 16u;
+
+  f32x4_t acc0[NSUB], acc1[NSUB];
 #pragma unroll
-  for (int i = 0; i < Acts<NSUB>::XP; ++i) {
-    const int m = (tid >> 5) + 8 * i;
-    act.off[i] = (m < rows) ? 2u * (uint32_t)((row0 + m) * I + kbase + (tid & 31) * 8)
-                            : kOutOfRange;
+  for (int s = 0; s < NSUB; ++s) {
+    acc0[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    acc1[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
-  Weights wt;
-  wt.rsrc = tm_buffer(w2 + (size_t)e * H * I, (uint32_t)((size_t)H * I * 2));
-  wt.off = 2u * (uint32_t)(n * I + kbase + g * 8);
+  u32x4_t a0[C::WLD], a1[C::WLD], b0[C::WLD], b1[C::WLD];
+  u32x4_t ah[C::NSTEP * NSUB], bh[C::NSTEP * NSUB];
 
-  f32x4_t acc[NSUB];
+  auto load = [&](u32x4_t (&w0r)[C::WLD], u32x4_t (&w1r)[C::WLD],
+                  u32x4_t (&hf)[C::NSTEP * NSUB], int c, bool valid) {
+    const uint32_t kstep0 = (uint32_t)c * C::NSTEP;
 #pragma unroll
-  for (int s = 0; s < NSUB; ++s) acc[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  u32x4_t wa[NSTEP], wb[NSTEP];
-  u32x4_t xr[Acts<NSUB>::XP];
-  uint16_t* L0 = lds;
-  uint16_t* L1 = lds + MT * LDS_LD;
-
-  auto compute = [&](const uint16_t* stage, const u32x4_t (&wr)[NSTEP]) {
-#pragma unroll
-    for (int s = 0; s < NSTEP; ++s) {
+    for (int s = 0; s < C::NSTEP; ++s)
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub)
-        acc[sub] = mfma16(lds_frag(stage, sub * 16 + r, s, g), wr[s], acc[sub]);
+        hf[s * NSUB + sub] = ld_b128<0>(
+            hr, valid ? hbase + ((uint32_t)sub * ksteps + kstep0 + s) * 1024u : kOutOfRange);
+    const uint32_t kb = (uint32_t)c * C::KC * 2u;
+    wr0.load(w0r, kb, valid);
+    wr1.load(w1r, kb, valid);
+  };
+  auto process = [&](const u32x4_t (&w0r)[C::WLD], const u32x4_t (&w1r)[C::WLD],
+                     const u32x4_t (&hf)[C::NSTEP * NSUB]) {
+    wr0.stage(scratch, w0r);
+    wr1.stage(scratch, w1r);
+#pragma unroll
+    for (int s = 0; s < C::NSTEP; ++s) {
+      const u32x4_t f0 = b_frag<NSUB>(scratch, lane, s);
+      const u32x4_t f1 = b_frag<NSUB>(scratch + ROWS * C::SROW, lane, s);
+#pragma unroll
+      for (int sub = 0; sub < NSUB; ++sub) {
+        acc0[sub] = mfma16(hf[s * NSUB + sub], f0, acc0[sub]);
+        acc1[sub] = mfma16(hf[s * NSUB + sub], f1, acc1[sub]);
+      }
     }
   };
 
-  const int nch = klen / KC;
-  act.load(xr, 0, true);
-  wt.load(wa, 0, true);
-  act.store(L0, xr);
-  tm_lds_barrier();
-  for (int c = 0; c + 1 < nch; c += 2) {
-    const uint32_t k1 = (uint32_t)(c + 1) * KC * 2;
-    act.load(xr, k1, true);
-    wt.load(wb, k1, true);
+  const int nch = klen / C::KC;
+  load(a0, a1, ah, wave, wave < nch);
+  for (int c = wave; c < nch; c += 2 * WAVES) {
+    const int c1 = c + WAVES;
+    load(b0, b1, bh, c1, c1 < nch);
     tm_sched_fence();
-    compute(L0, wa);
-    act.store(L1, xr);
-    tm_lds_barrier();
-    const bool more = (c + 2) < nch;
-    const uint32_t k2 = (uint32_t)(c + 2) * KC * 2;
-    act.load(xr, k2, more);
-    wt.load(wa, k2, more);
+    process(a0, a1, ah);
+    const int c2 = c1 + WAVES;
+    load(a0, a1, ah, c2, c2 < nch);
     tm_sched_fence();
-    compute(L1, wb);
-    act.store(L0, xr);
-    tm_lds_barrier();
+    process(b0, b1, bh);
   }
-  if (nch & 1) compute(L0, wa);
 
+  __syncthreads();
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(lds);
 #pragma unroll
   for (int sub = 0; sub < NSUB; ++sub) {
+    red[((wave * NSUB + sub) * 2 + 0) * 64 + lane] = acc0[sub];
+    red[((wave * NSUB + sub) * 2 + 1) * 64 + lane] = acc1[sub];
+  }
+  __syncthreads();
+  if (wave < NSUB) {
+    const int sub = wave;
+    const f32x4_t s0 = reduce_partials(red, NSUB, sub, 0, 2, lane);
+    const f32x4_t s1 = reduce_partials(red, NSUB, sub, 1, 2, lane);
+    const int r = lane & 15, g = lane >> 4;
+    const int n = ng * 2 * ROWS + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = sub * 16 + g * 4 + i;
       if (m < rows) {
         const int p = row0 + m;
         const float gate = gates_flat[sorted_slots[p]];
-        y[((size_t)split * R + p) * H + n] = acc[sub][i] * gate;
+        float* yr = y + ((size_t)split * R + p) * H;
+        yr[n] = s0[i] * gate;
+        yr[n + ROWS] = s1[i] * gate;
       }
     }
   }
 }
 
 __global__ void __launch_bounds__(256, 2)
-tm_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restrict__ w2,
+tm_gemm2_kernel(const uint16_t* __restrict__ hsw, const uint16_t* __restrict__ w2,
                 float* __restrict__ y, const float* __restrict__ gates_flat,
                 const int32_t* __restrict__ sorted_slots, const int32_t* __restrict__ tiles,
                 int R, int H, int I, int klen, uint32_t h_bytes) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2 * MT * LDS_LD];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kScratchBytes];
   const int tile = blockIdx.z;
   const int e = tiles[4 * tile];
   if (e < 0) return;
   const int row0 = tiles[4 * tile + 1];
   const int rows = tiles[4 * tile + 2];
   switch ((rows + 15) >> 4) {
-    case 1: gemm2_body<1>(lds, h, w2, y, gates_flat, sorted_slots, e, row0, rows, R, H, I, klen, h_bytes); break;
-    case 2: gemm2_body<2>(lds, h, w2, y, gates_flat, sorted_slots, e, row0, rows, R, H, I, klen, h_bytes); break;
-    case 3: gemm2_body<3>(lds, h, w2, y, gates_flat, sorted_slots, e, row0, rows, R, H, I, klen, h_bytes); break;
-    default: gemm2_body<4>(lds, h, w2, y, gates_flat, sorted_slots, e, row0, rows, R, H, I, klen, h_bytes); break;
+    case 1: gemm2_item<1>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
+    case 2: gemm2_item<2>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
+    case 3: gemm2_item<3>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
+    default: gemm2_item<4>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
   }
 }
+
+static_assert(kScratchBytes >= WAVES * 2 * ROWS * Cfg<1>::SROW, "gemm1 scratch");
+static_assert(kScratchBytes >= WAVES * 4 * 2 * 64 * 16, "gemm1 reduction");
 
 // --------------------------------------------------------------- combine --
 // out[t, n] = bf16( sum over (k = 0, 1) of sum over split s of y[s, pos(2t+k), n] ),
@@ -342,12 +415,14 @@ extern "C" int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void*
                             int64_t max_tiles, int64_t T, int64_t H, int64_t I, int64_t E,
                             void* stream) {
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS) return TM_ERR_SHAPE;
-  if (H < KC || (H % KC) != 0 || I < BN || (I % BN) != 0 || max_tiles < 1) return TM_ERR_SHAPE;
-  if (I * H * 2 >= (int64_t)kOutOfRange || T * H * 2 >= (int64_t)kOutOfRange)
+  if (H < 256 || (H % 256) != 0 || I < 256 || (I % 256) != 0 || max_tiles < 1)
     return TM_ERR_SHAPE;
-  if (!aligned16(x) || !aligned16(w1) || !aligned16(w3)) return TM_ERR_ALIGN;
-  const dim3 grid((unsigned)(I / BN), (unsigned)max_tiles);
-  hipLaunchKernelGGL(tm_gemm1_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+  if (I * H * 2 >= (int64_t)kOutOfRange || T * H * 2 >= (int64_t)kOutOfRange ||
+      max_tiles * MT * I * 2 >= (int64_t)kOutOfRange)
+    return TM_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(w3) || !aligned16(h)) return TM_ERR_ALIGN;
+  const dim3 grid((unsigned)(I / ROWS), (unsigned)max_tiles);
+  hipLaunchKernelGGL(tm_gemm1_kernel, grid, dim3(64 * WAVES), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)w1, (const uint16_t*)w3,
                      (uint16_t*)h, sorted_slots, tiles, (int)H, (int)I,
                      (uint32_t)(T * H * 2));
@@ -362,15 +437,17 @@ extern "C" int tm_op1_gemm2(const void* h, const void* w2, float* y,
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS) return TM_ERR_SHAPE;
   if (split < 1 || (I % split) != 0) return TM_ERR_SHAPE;
   const int64_t klen = I / split;
-  if (klen < KC || (klen % KC) != 0 || H < BN || (H % BN) != 0 || max_tiles < 1) return TM_ERR_SHAPE;
-  if (H * I * 2 >= (int64_t)kOutOfRange || 2 * T * I * 2 >= (int64_t)kOutOfRange)
+  if (klen < 256 || (klen % 256) != 0 || H < 2 * ROWS || (H % (2 * ROWS)) != 0 ||
+      max_tiles < 1)
+    return TM_ERR_SHAPE;
+  if (H * I * 2 >= (int64_t)kOutOfRange || max_tiles * MT * I * 2 >= (int64_t)kOutOfRange)
     return TM_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w2)) return TM_ERR_ALIGN;
-  const dim3 grid((unsigned)(H / BN), (unsigned)split, (unsigned)max_tiles);
-  hipLaunchKernelGGL(tm_gemm2_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+  const dim3 grid((unsigned)(H / (2 * ROWS)), (unsigned)split, (unsigned)max_tiles);
+  hipLaunchKernelGGL(tm_gemm2_kernel, grid, dim3(64 * WAVES), 0, (hipStream_t)stream,
                      (const uint16_t*)h, (const uint16_t*)w2, y, gates_flat, sorted_slots,
                      tiles, (int)(2 * T), (int)H, (int)I, (int)klen,
-                     (uint32_t)(2 * T * I * 2));
+                     (uint32_t)(max_tiles * MT * I * 2));
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }

@@ -28,8 +28,10 @@ if BM not in {16, 32}:
     raise ValueError("TREEMOE_BLOCK_M must be 16 or 32")
 
 # K segments of the down projection.  Each segment is one deterministic
-# partial; more segments = more workgroups in flight, more partial traffic.
-SPLIT_K = 4
+# partial; more segments = more, shorter workgroups and more partial traffic.
+# 2 is the measured optimum at the Mixtral shape on MI355X (1: 516 us,
+# 2: 497 us, 4: 517 us per layer at T=64, B=8).
+SPLIT_K = 2
 TILE_M = TM_GEMM_TILE_M
 
 
@@ -46,7 +48,7 @@ def compact_block_capacity(num_slots: int, expert_budget: int, block_m: int = BM
 
 
 def _split_for(inter: int) -> int:
-    for s in (SPLIT_K, 4, 2, 1):
+    for s in (SPLIT_K, 2, 1):
         if s >= 1 and inter % s == 0 and (inter // s) % 256 == 0:
             return s
     raise ValueError("intermediate size must be a multiple of 256")
@@ -85,7 +87,8 @@ class _Workspace:
         self.split = _split_for(inter)
         i32, i64, f32 = torch.int32, torch.int64, torch.float32
         self.router_gates = torch.empty(n, e, dtype=f32, device=device)
-        self.h = torch.empty(2 * n, inter, dtype=dtype, device=device)
+        # gate/up output, tile-swizzled: max_tiles x 64 rows x inter (A-fragment order)
+        self.h = torch.empty(self.max_tiles * TILE_M, inter, dtype=dtype, device=device)
         self.partial = torch.zeros(self.split, 2 * n, hidden, dtype=f32, device=device)
         self.topk_flat = torch.zeros(2 * n, dtype=i64, device=device)
         self.gates_flat = torch.zeros(2 * n, dtype=f32, device=device)
@@ -351,7 +354,8 @@ def tree_moe_forward(
         routing = route_experts(x, router_weight, node_accept_prob, expert_budget, inter,
                                 routing_objective=routing_objective)
     ws = routing.ws
-    if ws.h.shape != (2 * n, inter) or ws.partial.shape[2] != hidden:
+    if (ws.h.shape != (ws.max_tiles * TILE_M, inter) or ws.partial.shape[2] != hidden
+            or routing.max_tiles > ws.max_tiles):
         raise ValueError("routing was computed for a different shape")
     stream = _capi.stream_of(x.device)
     call("tm_op1_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h), ptr(routing.sorted_slots),
