@@ -94,14 +94,13 @@ int tm_op1_route_bucket(const float* gates, const float* accept, int64_t T,
                         int32_t* slot_pos, int32_t* tiles, void* stream);
 
 /*
- * Router + budget routing + bucketing in ONE launch: one workgroup per token
- * computes that token's gates exactly as tm_op1_router_gates; the last
- * workgroup to finish then buckets all tokens exactly as tm_op1_route_bucket.
- * Replaces the reference's router (op1_tree_moe.py:676-677) plus
- * `_budget_bucket_fused_kernel` (:159-297) as launched by `route_experts`
- * (:641-708).  Arguments and outputs are the union of the two entry points
- * above (gates [T, E] fp32 is written too); `counter` is one u32 of device
- * memory that must be zero before the first call and is left zero.
+ * Router + budget routing + bucketing in one call (two launches on `stream`:
+ * one workgroup per token computes that token's gates exactly as
+ * tm_op1_router_gates, then one workgroup buckets all tokens exactly as
+ * tm_op1_route_bucket).  Replaces the reference's router
+ * (op1_tree_moe.py:676-677) plus `_budget_bucket_fused_kernel` (:159-297) as
+ * launched by `route_experts` (:641-708).  Arguments and outputs are the union
+ * of the two entry points above; gates [T, E] fp32 is written too.
  */
 int tm_op1_route(const void* x, const void* wg, const float* accept, int64_t T,
                  int64_t H, int64_t E, int64_t budget, float tau, int objective,
@@ -110,7 +109,7 @@ int tm_op1_route(const void* x, const void* wg, const float* accept, int64_t T,
                  int64_t* padded_slots, int64_t* block_expert_ids,
                  int64_t* slot_to_row, float* demand, int32_t* expert_offsets,
                  int32_t* sorted_slots, int32_t* slot_pos, int32_t* tiles,
-                 uint32_t* counter, void* stream);
+                 void* stream);
 
 /*
  * Gate/up projection + SwiGLU for every routed slot.

@@ -70,7 +70,7 @@ def test_fused_route_argument_errors():
 
     fn = _capi.lib().tm_op1_route
     # x = 8 is misaligned, so every case below fails a check before any launch
-    base = [8, 0, 0, 64, 4096, 8, 4, ctypes.c_float(0.05), 0, 16, 16, 11] + [0] * 13
+    base = [8, 0, 0, 64, 4096, 8, 4, ctypes.c_float(0.05), 0, 16, 16, 11] + [0] * 12
     assert fn(*base) == 1002
     args = list(base)
     args[4] = 4095

@@ -116,9 +116,8 @@ def test_bucket_from_given_gates_bit_exact(t, budget):
         assert np.array_equal(demand.cpu().numpy().view(np.uint32), ref.demand.view(np.uint32))
 
 
-def test_fused_route_repeated_calls_reset_counter():
-    """The fused routing launch leaves its completion counter at zero, so
-    back-to-back calls of different sizes stay correct."""
+def test_route_repeated_calls_of_different_sizes():
+    """Back-to-back routing calls of different sizes reuse nothing stale."""
     _say("fused route repeated")
     m = _op1()
     for t in (64, 5, 64, 300, 1):
@@ -128,7 +127,6 @@ def test_fused_route_repeated_calls_reset_counter():
         ref = oracle_c.route_bucket(gates, accept.numpy(), 4)
         assert np.array_equal(r.topk_ids.reshape(-1).cpu().numpy(), ref.topk_ids)
         assert np.array_equal(r.tiles.cpu().numpy(), ref.tiles)
-    assert int(r.ws.counter.item()) == 0
 
 
 @pytest.mark.parametrize("budget", [2, 4, 8])

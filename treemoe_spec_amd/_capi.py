@@ -22,7 +22,7 @@ F32 = ctypes.c_float
 SIGNATURES: dict[str, list] = {
     "tm_op1_router_gates": [P, P, I64, I64, I64, P, P],
     "tm_op1_route_bucket": [P, P, I64, I64, I64, F32, I32, I64, I64, I64] + [P] * 10 + [P],
-    "tm_op1_route": [P, P, P, I64, I64, I64, I64, F32, I32, I64, I64, I64] + [P] * 12 + [P],
+    "tm_op1_route": [P, P, P, I64, I64, I64, I64, F32, I32, I64, I64, I64] + [P] * 11 + [P],
     "tm_op1_gemm1": [P, P, P, P, P, P, I64, I64, I64, I64, I64, P],
     "tm_op1_gemm2": [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
     "tm_op1_combine": [P, P, P, I64, I64, I64, P],

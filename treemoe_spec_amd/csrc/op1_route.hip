@@ -6,9 +6,10 @@
 // for bit: expert ids, gate weights, demand and every layout index.
 //
 // Launch shapes: the router runs one workgroup (8 waves) per token, one wave
-// per expert.  The bucketing runs in one workgroup; in the fused entry point
-// it is the last router workgroup to finish (a device-scope counter that the
-// kernel returns to zero), so routing costs a single launch.
+// per expert; the bucketing runs in one workgroup.  They are two launches:
+// handing the gates to a last-finishing workgroup instead would need a
+// device-scope release fence per workgroup (an L2 write-back), which measured
+// slower than the kernel boundary.
 #pragma clang fp contract(off)
 
 #include "tm_common.h"
@@ -99,7 +100,11 @@ struct BucketArgs {
   int32_t* tiles;
 };
 
+constexpr int kStageFloats = 16384;  // gates staged in LDS when T * E fits (64 KB)
+
 struct BucketShared {
+  float gates[kStageFloats];
+  float accept[TM_MAX_TOKENS];
   float demand[TM_MAX_EXPERTS];
   float crit[TM_MAX_EXPERTS];
   int keep[TM_MAX_EXPERTS];
@@ -110,6 +115,18 @@ struct BucketShared {
   uint8_t fe[kMaxSlots];
   uint16_t cnt[kMaxChunks * TM_MAX_EXPERTS];
 };
+
+// Wave-wide exclusive prefix sum (lane order).
+__device__ __forceinline__ int wave_exclusive_scan(int v, int lane, int* total) {
+  int inc = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(inc, off);
+    if (lane >= off) inc += u;
+  }
+  *total = __shfl(inc, 63);
+  return inc - v;
+}
 
 // Budget routing and bucketing for all T tokens in one workgroup.
 //
@@ -123,9 +140,13 @@ struct BucketShared {
 //  3. per token: top-2 of the kept gates (ties to the lower expert id, the
 //     second pick excludes the first), weights p_k / (p1 + p2), and (1, 0) when
 //     accept < tau (tree_moe_ref.py:51-66).
-//  4. slot s = 2t + k; stable rank inside its expert from wave ballots; the
-//     reference's padded BM-row block layout (op1_tree_moe.py:111-144) and the
-//     compact expert-major order with its GEMM tile list.
+//  4. slot s = 2t + k; stable rank inside its expert from wave ballots and a
+//     scan over 64-slot chunks; the reference's padded BM-row block layout
+//     (op1_tree_moe.py:111-144) and the compact expert-major order with its
+//     GEMM tile list.
+// Gates and accept are staged in LDS first; every serial step is a wave-wide
+// reduction or scan (one lane per expert), so no single thread walks a
+// dependent chain of LDS or global loads.
 __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -135,10 +156,20 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   const int nchunk = (nslot + 63) >> 6;
   const int padded_rows = a.max_blocks * a.BM;
   const bool critical = a.objective == TM_OBJECTIVE_CRITICAL_PATH;
+  const bool staged = T * E <= kStageFloats;
+
+  // 0. stage gates and accept
+  if (staged) {
+    for (int i = tid; i < T * E; i += kThreads) sh.gates[i] = a.gates[i];
+  }
+  for (int t = tid; t < T; t += kThreads) sh.accept[t] = a.accept[t];
+  for (int i = tid; i < padded_rows; i += kThreads) a.padded_slots[i] = -1;
+  __syncthreads();
+  const float* G = staged ? sh.gates : a.gates;
 
   if (critical) {
     for (int t = tid; t < T; t += kThreads) {
-      const float* g = a.gates + (size_t)t * E;
+      const float* g = G + (size_t)t * E;
       int u1 = 0;
       float b1 = g[0];
       for (int e = 1; e < E; ++e) {
@@ -163,8 +194,8 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     float acc = 0.0f;
     float crit = -INFINITY;
     for (int t = lane; t < T; t += 64) {
-      const float av = a.accept[t];
-      const float p = av * a.gates[(size_t)t * E + e];
+      const float av = sh.accept[t];
+      const float p = av * G[(size_t)t * E + e];
       acc = acc + p;
       if (critical) {
         const bool needed = (sh.fe[2 * t] == e) || ((sh.fe[2 * t + 1] == e) && (av >= a.tau));
@@ -182,35 +213,46 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
       a.demand_out[e] = acc;
     }
   }
-  // fill the padded layout while the keep set is chosen (scattered into below)
-  for (int i = tid; i < padded_rows; i += kThreads) a.padded_slots[i] = -1;
   __syncthreads();
 
-  // 2. keep set: selection in lexicographic order, first occurrence on ties.
-  if (tid == 0) {
-    for (int e = 0; e < E; ++e) sh.keep[e] = 0;
-    for (int rank = 0; rank < a.budget; ++rank) {
-      int best = -1;
-      for (int e = 0; e < E; ++e) {
-        if (sh.keep[e]) continue;
-        if (best < 0) { best = e; continue; }
-        bool better;
-        if (critical) {
-          better = (sh.crit[e] > sh.crit[best]) ||
-                   (sh.crit[e] == sh.crit[best] && sh.demand[e] > sh.demand[best]);
+  // 2. keep set (wave 0, lane = expert): `budget` rounds of a wave-wide argmax
+  //    in the order (crit desc,) demand desc, expert asc.
+  if (wave == 0) {
+    const bool valid = lane < E;
+    const float d = valid ? sh.demand[lane] : 0.0f;
+    const float c = (valid && critical) ? sh.crit[lane] : 0.0f;
+    bool kept = false;
+    for (int r = 0; r < a.budget; ++r) {
+      int av = (valid && !kept) ? 1 : 0;
+      float bc = c, bd = d;
+      int be = lane;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const int oav = __shfl_xor(av, off);
+        const float oc = __shfl_xor(bc, off);
+        const float od = __shfl_xor(bd, off);
+        const int oe = __shfl_xor(be, off);
+        bool take;
+        if (oav != av) {
+          take = oav != 0;
+        } else if (critical && oc != bc) {
+          take = oc > bc;
+        } else if (od != bd) {
+          take = od > bd;
         } else {
-          better = sh.demand[e] > sh.demand[best];
+          take = oe < be;
         }
-        if (better) best = e;
+        if (take) { av = oav; bc = oc; bd = od; be = oe; }
       }
-      sh.keep[best] = 1;
+      if (lane == be) kept = true;
     }
+    if (valid) sh.keep[lane] = kept ? 1 : 0;
   }
   __syncthreads();
 
   // 3. in-budget top-2, renormalisation, low-acceptance degrade
   for (int t = tid; t < T; t += kThreads) {
-    const float* g = a.gates + (size_t)t * E;
+    const float* g = G + (size_t)t * E;
     int i1 = -1;
     float g1 = 0.0f;
     for (int e = 0; e < E; ++e) {
@@ -227,12 +269,12 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     const float s = g1 + g2;
     float tg1 = g1 / s;
     float tg2 = g2 / s;
-    if (a.accept[t] < a.tau) { tg1 = 1.0f; tg2 = 0.0f; }
+    if (sh.accept[t] < a.tau) { tg1 = 1.0f; tg2 = 0.0f; }
     a.topk_ids[2 * t] = i1;
     a.topk_ids[2 * t + 1] = i2;
     a.gates_flat[2 * t] = tg1;
     a.gates_flat[2 * t + 1] = tg2;
-    sh.fe[2 * t] = (uint8_t)i1;  // the critical-path use of fe ended at the barrier above
+    sh.fe[2 * t] = (uint8_t)i1;  // the critical-path use of fe ended at an earlier barrier
     sh.fe[2 * t + 1] = (uint8_t)i2;
   }
   __syncthreads();
@@ -247,42 +289,49 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     }
   }
   __syncthreads();
-  // 4b. exclusive scan over chunks (slot order) for every expert
-  if (tid < E) {
-    int run = 0;
-    for (int q = 0; q < nchunk; ++q) {
-      const int c = sh.cnt[q * TM_MAX_EXPERTS + tid];
-      sh.cnt[q * TM_MAX_EXPERTS + tid] = (uint16_t)run;
-      run += c;
-    }
-    sh.count[tid] = run;
+  // 4b. exclusive scan over chunks (slot order) per expert; chunks q and q+64
+  //     of one expert sit in lane q of the wave that owns the expert.
+  for (int e = wave; e < E; e += kWaves) {
+    const int v0 = (lane < nchunk) ? (int)sh.cnt[lane * TM_MAX_EXPERTS + e] : 0;
+    const int v1 = (lane + 64 < nchunk) ? (int)sh.cnt[(lane + 64) * TM_MAX_EXPERTS + e] : 0;
+    int tot0, tot1;
+    const int x0 = wave_exclusive_scan(v0, lane, &tot0);
+    const int x1 = wave_exclusive_scan(v1, lane, &tot1);
+    if (lane < nchunk) sh.cnt[lane * TM_MAX_EXPERTS + e] = (uint16_t)x0;
+    if (lane + 64 < nchunk) sh.cnt[(lane + 64) * TM_MAX_EXPERTS + e] = (uint16_t)(tot0 + x1);
+    if (lane == 0) sh.count[e] = tot0 + tot1;
   }
   __syncthreads();
-  // 4c. block layout (reference), compact offsets and GEMM tiles
-  if (tid == 0) {
-    int blocks = 0;
-    int off = 0;
-    int j = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = sh.count[e];
-      const int nb = (c + a.BM - 1) / a.BM;
-      sh.block_start[e] = blocks;
-      sh.nblocks[e] = nb;
-      blocks += nb;
-      sh.offset[e] = off;
-      for (int r = 0; r < c; r += TM_GEMM_TILE_M) {
+  // 4c. block layout (reference), compact offsets and GEMM tiles (wave 0,
+  //     lane = expert)
+  if (wave == 0) {
+    const int c = (lane < E) ? sh.count[lane] : 0;
+    const int nb = (c + a.BM - 1) / a.BM;
+    const int nt = (c + TM_GEMM_TILE_M - 1) / TM_GEMM_TILE_M;
+    int tot_off, tot_blk, tot_tiles;
+    const int off = wave_exclusive_scan(c, lane, &tot_off);
+    const int bs = wave_exclusive_scan(nb, lane, &tot_blk);
+    const int ts = wave_exclusive_scan(nt, lane, &tot_tiles);
+    if (lane < E) {
+      sh.offset[lane] = off;
+      sh.block_start[lane] = bs;
+      sh.nblocks[lane] = nb;
+      a.expert_offsets[lane] = off;
+      for (int k = 0; k < nt; ++k) {
+        const int j = ts + k;
         if (j < a.max_tiles) {
-          a.tiles[4 * j + 0] = e;
-          a.tiles[4 * j + 1] = off + r;
-          a.tiles[4 * j + 2] = min(TM_GEMM_TILE_M, c - r);
+          a.tiles[4 * j + 0] = lane;
+          a.tiles[4 * j + 1] = off + k * TM_GEMM_TILE_M;
+          a.tiles[4 * j + 2] = min(TM_GEMM_TILE_M, c - k * TM_GEMM_TILE_M);
           a.tiles[4 * j + 3] = 0;
         }
-        ++j;
       }
-      off += c;
     }
-    sh.offset[E] = off;
-    for (; j < a.max_tiles; ++j) {
+    if (lane == 0) {
+      sh.offset[E] = tot_off;
+      a.expert_offsets[E] = tot_off;
+    }
+    for (int j = tot_tiles + lane; j < a.max_tiles; j += 64) {
       a.tiles[4 * j + 0] = -1;
       a.tiles[4 * j + 1] = 0;
       a.tiles[4 * j + 2] = 0;
@@ -290,7 +339,6 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     }
   }
   __syncthreads();
-  if (tid <= E) a.expert_offsets[tid] = sh.offset[tid];
   // 4d. stable in-expert rank -> destinations
   for (int q = wave; q < nchunk; q += kWaves) {
     const int s = q * 64 + lane;
@@ -330,26 +378,6 @@ tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg
 __global__ void __launch_bounds__(kThreads) tm_bucket_kernel(BucketArgs args) {
   __shared__ BucketShared sh;
   bucket_all(args, sh);
-}
-
-// Router for token blockIdx.x, then the last workgroup to finish buckets all
-// tokens.  `counter` is zero on entry and is returned to zero by that
-// workgroup.
-__global__ void __launch_bounds__(kThreads)
-tm_route_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg, int H,
-                BucketArgs args, float* __restrict__ gates, uint32_t* __restrict__ counter) {
-  __shared__ float s_logit[TM_MAX_EXPERTS];
-  __shared__ BucketShared sh;
-  __shared__ int s_last;
-  router_token(x, wg, gates, blockIdx.x, H, args.E, s_logit);
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = (atomicAdd(counter, 1u) == gridDim.x - 1u);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  bucket_all(args, sh);
-  if (threadIdx.x == 0) *counter = 0u;
 }
 
 int check_bucket_args(int64_t T, int64_t E, int64_t budget, int objective, int64_t block_m,
@@ -432,7 +460,7 @@ extern "C" int tm_op1_route(const void* x, const void* wg, const float* accept, 
                             int64_t* padded_slots, int64_t* block_expert_ids,
                             int64_t* slot_to_row, float* demand, int32_t* expert_offsets,
                             int32_t* sorted_slots, int32_t* slot_pos, int32_t* tiles,
-                            uint32_t* counter, void* stream) {
+                            void* stream) {
   const int rc = check_bucket_args(T, E, budget, objective, block_m, max_blocks, max_tiles);
   if (rc != TM_OK) return rc;
   if (H < 8 || (H % 8) != 0) return TM_ERR_SHAPE;
@@ -441,9 +469,11 @@ extern "C" int tm_op1_route(const void* x, const void* wg, const float* accept, 
                                  max_tiles, topk_ids, gates_flat, padded_slots,
                                  block_expert_ids, slot_to_row, demand, expert_offsets,
                                  sorted_slots, slot_pos, tiles);
-  hipLaunchKernelGGL(tm_route_kernel, dim3((unsigned)T), dim3(kThreads), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)wg, (int)H, a,
-                     gates, counter);
+  hipLaunchKernelGGL(tm_router_kernel, dim3((unsigned)T), dim3(kThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)wg, gates, (int)T,
+                     (int)H, (int)E);
+  TM_HIP_CHECK_LAUNCH();
+  hipLaunchKernelGGL(tm_bucket_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, a);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }

@@ -100,7 +100,6 @@ class _Workspace:
         self.sorted_slots = torch.zeros(2 * n, dtype=i32, device=device)
         self.slot_pos = torch.zeros(2 * n, dtype=i32, device=device)
         self.tiles = torch.zeros(self.max_tiles, 4, dtype=i32, device=device)
-        self.counter = torch.zeros(1, dtype=i32, device=device)
 
 
 _ws_cache: dict[tuple, _Workspace] = {}
@@ -131,24 +130,13 @@ def _launch_route_bucket(gates, accept, n, e, budget, tau, objective, block_m, m
 
 def _launch_route(x, router_weight, accept, budget, tau, objective, block_m, max_blocks,
                   max_tiles, gates, topk, gates_flat, padded, blk, s2r, demand, offsets,
-                  sorted_slots, slot_pos, tiles, counter) -> None:
+                  sorted_slots, slot_pos, tiles) -> None:
     n, hidden = x.shape
     call("tm_op1_route", ptr(x), ptr(router_weight), ptr(accept), n, hidden,
          router_weight.shape[0], budget, float(tau), TM_OBJECTIVE[objective], block_m,
          max_blocks, max_tiles, ptr(gates), ptr(topk), ptr(gates_flat), ptr(padded), ptr(blk),
          ptr(s2r), ptr(demand), ptr(offsets), ptr(sorted_slots), ptr(slot_pos), ptr(tiles),
-         ptr(counter), _capi.stream_of(x.device))
-
-
-_counters: dict[int, torch.Tensor] = {}
-
-
-def _counter(device: torch.device) -> torch.Tensor:
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    c = _counters.get(idx)
-    if c is None:
-        c = _counters[idx] = torch.zeros(1, dtype=torch.int32, device=device)
-    return c
+         _capi.stream_of(x.device))
 
 
 def _prep_accept(node_accept_prob: torch.Tensor, n: int) -> torch.Tensor:
@@ -201,8 +189,7 @@ def route_and_bucket(
         gates = torch.empty(n, e, dtype=torch.float32, device=dev)
         _launch_route(x, router_weight, accept, expert_budget, top1_threshold,
                       routing_objective, block_m, max_blocks, max_tiles, gates, topk, gflat,
-                      padded, blk, s2r, demand, offsets, sorted_slots, slot_pos, tiles,
-                      _counter(dev))
+                      padded, blk, s2r, demand, offsets, sorted_slots, slot_pos, tiles)
     else:
         gates = router_gates.float().contiguous()
         _launch_route_bucket(gates, accept, n, e, expert_budget, top1_threshold,
@@ -315,7 +302,7 @@ def route_experts(
     _launch_route(x, router_weight, accept, expert_budget, top1_threshold, routing_objective,
                   BM, max_blocks, max_tiles, ws.router_gates, ws.topk_flat, ws.gates_flat,
                   padded, blk, ws.slot_to_row, ws.demand, ws.expert_offsets, ws.sorted_slots,
-                  ws.slot_pos, tiles, ws.counter)
+                  ws.slot_pos, tiles)
     return Routing(ws, ws.router_gates, ws.topk_flat.view(n, 2), ws.gates_flat, padded, blk,
                    ws.slot_to_row, max_blocks, launch_blocks, ws.demand, ws.expert_offsets,
                    ws.sorted_slots, ws.slot_pos, tiles, max_tiles)
