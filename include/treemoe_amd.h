@@ -43,6 +43,7 @@ extern "C" {
 #define TM_MAX_EXPERTS 64
 #define TM_MAX_TOKENS 4096
 #define TM_GEMM_TILE_M 64      /* rows of one expert processed per GEMM tile */
+#define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
 
 /* ABI version (major*10000 + minor*100 + patch). */
 int tm_version(void);
@@ -152,7 +153,9 @@ int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
 /* ---------------------------------------------------------------- op4 -- */
 
 /*
- * First-occurrence argmax per tree node + greedy accept walk, one launch.
+ * First-occurrence argmax per tree node + greedy accept walk (two launches on
+ * `stream`: row ranges of ~4 KiB scanned by one workgroup each, then one
+ * workgroup that reduces the ranges and walks the tree from LDS).
  * Replaces `_argmax_kernel` (treemoe/kernels/op4_commit.py:82-96) and
  * `_tree_verify_greedy_kernel` (:99-131) plus the result glue (:223-239).
  *
@@ -160,11 +163,11 @@ int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
  * TM_DTYPE_BF16.  NaN ranks above every number (first NaN wins), as in
  * torch.argmax.  tokens [N] i64; children in CSR form: child_start [N] i32,
  * child_count [N] i32, child_list [max(1, N-1)] i32.  The walk visits at most
- * max_depth levels.
+ * max_depth levels (and accepts at most N nodes).
  * Outputs: argmax [N] i32, accepted_slots [N] i64 (-1 pad), accepted_tokens
  * [N] i64 (-1 pad), result [3] i64 = (bonus_token, num_accepted, next_root).
- * `counter` is one u32 of device memory that must be zero before the first
- * call; the kernel leaves it zero again.
+ * `workspace`: N * TM_OP4_MAX_PARTS * 8 bytes of device memory, 8-byte
+ * aligned, no initial contents required.
  */
 int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
                        int64_t row_stride, const int64_t* tokens,
@@ -172,7 +175,7 @@ int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
                        const int32_t* child_list, int64_t max_depth,
                        int32_t* argmax, int64_t* accepted_slots,
                        int64_t* accepted_tokens, int64_t* result,
-                       uint32_t* counter, void* stream);
+                       void* workspace, void* stream);
 
 /*
  * Paged KV commit of [root] + accepted path.  Replaces `_kv_commit_kernel` and

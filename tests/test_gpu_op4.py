@@ -34,7 +34,8 @@ def _tree(seed, n, vocab, max_depth=None):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("n,v", [(16, 512), (64, 32000), (3, 7), (5, 1000), (64, 32001)])
+@pytest.mark.parametrize("n,v", [(16, 512), (64, 32000), (3, 7), (5, 1000), (64, 32001),
+                                 (6, 300001)])
 def test_argmax_first_occurrence(dtype, n, v):
     _say(f"argmax {dtype} n={n} v={v}")
     op4 = _op4()
@@ -71,7 +72,7 @@ def test_argmax_first_occurrence(dtype, n, v):
 
 def _direct_argmax(logits, argmax):
     from treemoe_spec_amd import _capi
-    from treemoe_spec_amd.kernels.op4_commit import _children_csr, _counter
+    from treemoe_spec_amd.kernels.op4_commit import _children_csr, argmax_workspace
 
     n, v = logits.shape
     dtype = _capi.TM_DTYPE_F32 if logits.dtype == torch.float32 else _capi.TM_DTYPE_BF16
@@ -82,8 +83,47 @@ def _direct_argmax(logits, argmax):
     _capi.call("tm_op4_argmax_walk", logits.data_ptr(), dtype, n, v, logits.stride(0),
                tokens.data_ptr(), csr.data_ptr(), csr.data_ptr() + 4 * n,
                csr.data_ptr() + 8 * n, 0, argmax.data_ptr(), out[0].data_ptr(),
-               out[1].data_ptr(), result.data_ptr(), _counter(logits.device).data_ptr(),
-               _capi.stream_of(logits.device))
+               out[1].data_ptr(), result.data_ptr(),
+               argmax_workspace(n, logits.device).data_ptr(), _capi.stream_of(logits.device))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_argmax_unaligned_rows(dtype):
+    """Rows that start off a 16-byte boundary take the scalar loads."""
+    n, v = 7, 5003
+    g = torch.Generator().manual_seed(11)
+    full = (torch.randn(n, v + 1, generator=g) * 3).to(dtype)
+    full[3, 4000] = full[3, 1:].max() + 1
+    full[3, 17] = full[3, 4000]
+    logits = full.cuda()[:, 1:]
+    assert logits.data_ptr() % 16 != 0 and logits.stride(0) == v + 1
+    argmax = torch.empty(n, dtype=torch.int32, device="cuda")
+    _direct_argmax(logits, argmax)
+    expect = full[:, 1:].float().argmax(-1).numpy()
+    assert np.array_equal(argmax.cpu().numpy(), expect)
+    assert int(argmax[3]) == 16
+
+
+def test_greedy_walk_large_tree_from_global_memory():
+    """A 2100-node chain (more nodes than the walk stages in LDS) is accepted
+    to the end."""
+    _say("walk n=2100 chain")
+    op4 = _op4()
+    n, v = 2100, 64
+    g = torch.Generator().manual_seed(5)
+    tokens = torch.randint(0, v, (n,), generator=g)
+    children = [[i + 1] for i in range(n - 1)] + [[]]
+    logits = torch.randn(n, v, generator=g)
+    for i in range(n - 1):
+        logits[i, int(tokens[i + 1])] = 50.0
+    res = op4.fused_verify_commit(logits.cuda(), None, tokens.cuda(), None, children,
+                                  max_depth=n)
+    c_slots, c_toks, c_bonus, c_num, _ = oracle_c.greedy_walk(
+        oracle_c.argmax(logits.numpy()), tokens.numpy(), children, n)
+    assert int(res.num_accepted) == c_num == n - 1
+    assert np.array_equal(res.accepted_slots.cpu().numpy(), c_slots)
+    assert np.array_equal(res.accepted_tokens.cpu().numpy(), c_toks)
+    assert int(res.bonus_token) == c_bonus
 
 
 @pytest.mark.parametrize("seed", range(50))

@@ -35,6 +35,7 @@ TM_OBJECTIVE = {"mass": 0, "critical_path": 1}
 TM_DTYPE_F32 = 0
 TM_DTYPE_BF16 = 1
 TM_GEMM_TILE_M = 64
+TM_OP4_MAX_PARTS = 64
 
 _lib = None
 

@@ -1,12 +1,14 @@
 // op4 on gfx950: first-occurrence argmax over the vocabulary for every tree
-// node, the greedy accept walk (run by the last workgroup to finish its row),
-// and the paged KV commit of [root] + accepted path.
+// node (row-chunked over many workgroups), the greedy accept walk from LDS in
+// one workgroup, and the paged KV commit of [root] + accepted path.
 #include "tm_common.h"
 
 namespace {
 
 constexpr int kArgThreads = 256;
-constexpr int kMaxPath = 2048;
+constexpr int kWalkThreads = 1024;
+constexpr int kChunkBytes = 4096;    // bytes of one row scanned by one workgroup
+constexpr int kStageNodes = 2048;    // trees up to this size are walked from LDS
 
 // (va, ia) ranks before (vb, ib): larger value first, NaN above every number,
 // equal values (and NaN vs NaN) go to the lower index.  This is the order in
@@ -27,75 +29,87 @@ struct Best {
   }
 };
 
-template <int kDtype>
-__device__ __forceinline__ Best scan_row(const void* logits, int64_t row_stride, int row, int V) {
-  Best b{-INFINITY, 0x7fffffff};
-  const int tid = threadIdx.x;
-  if (kDtype == TM_DTYPE_F32) {
-    const float* p = reinterpret_cast<const float*>(logits) + (size_t)row * row_stride;
-    const bool vec = ((uintptr_t)p % 16) == 0;
-    int done = 0;
-    if (vec) {
-      const int nv = V >> 2;
-      const float4* p4 = reinterpret_cast<const float4*>(p);
-      for (int q = tid; q < nv; q += kArgThreads) {
-        const float4 v = p4[q];
-        b.offer(v.x, 4 * q);
-        b.offer(v.y, 4 * q + 1);
-        b.offer(v.z, 4 * q + 2);
-        b.offer(v.w, 4 * q + 3);
-      }
-      done = nv << 2;
-    }
-    for (int q = done + tid; q < V; q += kArgThreads) b.offer(p[q], q);
-  } else {
-    const uint16_t* p = reinterpret_cast<const uint16_t*>(logits) + (size_t)row * row_stride;
-    const bool vec = ((uintptr_t)p % 16) == 0;
-    int done = 0;
-    if (vec) {
-      const int nv = V >> 3;
-      const uint4* p8 = reinterpret_cast<const uint4*>(p);
-      for (int q = tid; q < nv; q += kArgThreads) {
-        const uint4 v = p8[q];
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          b.offer(__uint_as_float(w[j] << 16), 8 * q + 2 * j);
-          b.offer(__uint_as_float(w[j] & 0xffff0000u), 8 * q + 2 * j + 1);
-        }
-      }
-      done = nv << 3;
-    }
-    for (int q = done + tid; q < V; q += kArgThreads) b.offer(tm_bf16_to_f32(p[q]), q);
-  }
-  return b;
-}
+struct Partial {
+  float v;
+  int i;
+};
 
-template <int kDtype>
-__global__ void __launch_bounds__(kArgThreads)
-tm_argmax_walk_kernel(const void* __restrict__ logits, int N, int V, int64_t row_stride,
-                      const int64_t* __restrict__ tokens, const int32_t* __restrict__ child_start,
-                      const int32_t* __restrict__ child_count,
-                      const int32_t* __restrict__ child_list, int max_depth,
-                      int32_t* __restrict__ argmax, int64_t* __restrict__ accepted_slots,
-                      int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result,
-                      uint32_t* __restrict__ counter) {
-  __shared__ float s_v[kArgThreads / 64];
-  __shared__ int s_i[kArgThreads / 64];
-  __shared__ int s_last;
-  __shared__ int s_count;
-  __shared__ int s_path[kMaxPath];
-
-  const int row = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  Best b = scan_row<kDtype>(logits, row_stride, row, V);
+__device__ __forceinline__ Best wave_best(Best b) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(b.v, off);
     const int oi = __shfl_xor(b.i, off);
     b.offer(ov, oi);
   }
+  return b;
+}
+
+// Elements [lo, hi) of one row.  `vec` rows are 16-byte aligned and lo is a
+// multiple of the vector width, so every thread issues its (at most
+// kChunkBytes / 16 / kArgThreads = 1) 16-byte load before any compare.
+template <int kDtype>
+__device__ __forceinline__ Best scan_range(const void* row_ptr, int lo, int hi, bool vec) {
+  Best b{-INFINITY, 0x7fffffff};
+  const int tid = threadIdx.x;
+  if (kDtype == TM_DTYPE_F32) {
+    const float* p = reinterpret_cast<const float*>(row_ptr);
+    int done = lo;
+    if (vec) {
+      const int nv = (hi - lo) >> 2;
+      const float4* p4 = reinterpret_cast<const float4*>(p + lo);
+      for (int q = tid; q < nv; q += kArgThreads) {
+        const float4 v = p4[q];
+        const int e = lo + 4 * q;
+        b.offer(v.x, e);
+        b.offer(v.y, e + 1);
+        b.offer(v.z, e + 2);
+        b.offer(v.w, e + 3);
+      }
+      done = lo + (nv << 2);
+    }
+    for (int q = done + tid; q < hi; q += kArgThreads) b.offer(p[q], q);
+  } else {
+    const uint16_t* p = reinterpret_cast<const uint16_t*>(row_ptr);
+    int done = lo;
+    if (vec) {
+      const int nv = (hi - lo) >> 3;
+      const uint4* p8 = reinterpret_cast<const uint4*>(p + lo);
+      for (int q = tid; q < nv; q += kArgThreads) {
+        const uint4 v = p8[q];
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        const int e = lo + 8 * q;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          b.offer(__uint_as_float(w[j] << 16), e + 2 * j);
+          b.offer(__uint_as_float(w[j] & 0xffff0000u), e + 2 * j + 1);
+        }
+      }
+      done = lo + (nv << 3);
+    }
+    for (int q = done + tid; q < hi; q += kArgThreads) b.offer(tm_bf16_to_f32(p[q]), q);
+  }
+  return b;
+}
+
+// grid (parts, N): workgroup (p, row) writes the best (value, index) of
+// elements [p * per_part, min(V, (p + 1) * per_part)) of `row` to
+// partial[row * parts + p].  An empty range writes (-inf, INT_MAX), which
+// every element ranks before.
+template <int kDtype>
+__global__ void __launch_bounds__(kArgThreads)
+tm_argmax_part_kernel(const void* __restrict__ logits, int V, int64_t row_stride, int per_part,
+                      int parts, int vec_ok, Partial* __restrict__ partial) {
+  __shared__ float s_v[kArgThreads / 64];
+  __shared__ int s_i[kArgThreads / 64];
+  const int p = blockIdx.x;
+  const int row = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const size_t elem = (kDtype == TM_DTYPE_F32) ? 4 : 2;
+  const char* row_ptr = reinterpret_cast<const char*>(logits) + (size_t)row * row_stride * elem;
+  const int lo = min(V, p * per_part);
+  const int hi = min(V, lo + per_part);
+  Best b = wave_best(scan_range<kDtype>(row_ptr, lo, hi, vec_ok != 0));
   if (lane == 0) {
     s_v[wave] = b.v;
     s_i[wave] = b.i;
@@ -104,46 +118,90 @@ tm_argmax_walk_kernel(const void* __restrict__ logits, int N, int V, int64_t row
   if (tid == 0) {
     Best r{s_v[0], s_i[0]};
     for (int w = 1; w < kArgThreads / 64; ++w) r.offer(s_v[w], s_i[w]);
-    argmax[row] = r.i;
-    __threadfence();
-    const uint32_t prev = atomicAdd(counter, 1u);
-    s_last = (prev == (uint32_t)(N - 1));
+    partial[(size_t)row * parts + p] = Partial{r.v, r.i};
+  }
+}
+
+struct WalkShared {
+  int64_t tokens[kStageNodes];
+  int argmax[kStageNodes];
+  int child_start[kStageNodes];
+  int child_count[kStageNodes];
+  int child_list[kStageNodes];
+  int count;
+};
+
+// One workgroup: reduce the row partials to argmax[N], then the greedy walk
+// from the root (op4_commit.py:99-131): at each level take the first child,
+// in child-list order, whose token equals the node's argmax.  Trees of at
+// most kStageNodes nodes are staged in LDS first, so the walk's dependent
+// reads are LDS reads; larger trees are walked from global memory.  The walk
+// also stops once N nodes are accepted (only a child list with a cycle gets
+// there), so accepted_slots is never written past N.
+__global__ void __launch_bounds__(kWalkThreads)
+tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
+               const int64_t* __restrict__ tokens, const int32_t* __restrict__ child_start,
+               const int32_t* __restrict__ child_count, const int32_t* __restrict__ child_list,
+               int max_depth, int32_t* __restrict__ argmax, int64_t* __restrict__ accepted_slots,
+               int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result) {
+  __shared__ WalkShared sh;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const bool staged = N <= kStageNodes;
+  const int nlist = N > 1 ? N - 1 : 1;
+  if (staged) {
+    for (int i = tid; i < N; i += kWalkThreads) {
+      sh.tokens[i] = tokens[i];
+      sh.child_start[i] = child_start[i];
+      sh.child_count[i] = child_count[i];
+    }
+    for (int i = tid; i < nlist; i += kWalkThreads) sh.child_list[i] = child_list[i];
+  }
+  for (int row = wave; row < N; row += kWalkThreads / 64) {
+    Best b{-INFINITY, 0x7fffffff};
+    for (int p = lane; p < parts; p += 64) {
+      const Partial q = partial[(size_t)row * parts + p];
+      b.offer(q.v, q.i);
+    }
+    b = wave_best(b);
+    if (lane == 0) {
+      argmax[row] = b.i;
+      if (staged) sh.argmax[row] = b.i;
+    }
   }
   __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // Greedy walk from the root (op4_commit.py:99-131): at each level take the
-  // first child, in child-list order, whose token equals the node's argmax.
+  const int64_t* tok = staged ? sh.tokens : tokens;
+  const int* am = staged ? sh.argmax : argmax;
+  const int* cs = staged ? sh.child_start : child_start;
+  const int* cc = staged ? sh.child_count : child_count;
+  const int* cl = staged ? sh.child_list : child_list;
   if (tid == 0) {
     int node = 0;
     int count = 0;
-    const int depth = max_depth < kMaxPath ? max_depth : kMaxPath;
-    for (int d = 0; d < depth; ++d) {
-      const int64_t target = (int64_t)__atomic_load_n(argmax + node, __ATOMIC_RELAXED);
-      const int st = child_start[node];
-      const int cnt = child_count[node];
+    for (int d = 0; d < max_depth && count < N; ++d) {
+      const int64_t target = (int64_t)am[node];
+      const int st = cs[node];
+      const int cnt = cc[node];
       int acc = -1;
       for (int j = 0; j < cnt; ++j) {
-        const int c = child_list[st + j];
-        if (tokens[c] == target) { acc = c; break; }
+        const int c = cl[st + j];
+        if (tok[c] == target) { acc = c; break; }
       }
       if (acc < 0) break;
-      s_path[count++] = acc;
+      accepted_slots[count] = acc;
+      accepted_tokens[count] = tok[acc];
+      ++count;
       node = acc;
     }
-    s_count = count;
-    result[0] = (int64_t)__atomic_load_n(argmax + node, __ATOMIC_RELAXED);
+    sh.count = count;
+    result[0] = (int64_t)am[node];
     result[1] = count;
     result[2] = node;
-    *counter = 0u;
   }
   __syncthreads();
-  const int count = s_count;
-  for (int i = tid; i < N; i += kArgThreads) {
-    const int slot = (i < count) ? s_path[i] : -1;
-    accepted_slots[i] = slot;
-    accepted_tokens[i] = (slot >= 0) ? tokens[slot] : -1;
+  for (int i = sh.count + tid; i < N; i += kWalkThreads) {
+    accepted_slots[i] = -1;
+    accepted_tokens[i] = -1;
   }
 }
 
@@ -189,23 +247,39 @@ extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int6
                                   const int32_t* child_start, const int32_t* child_count,
                                   const int32_t* child_list, int64_t max_depth,
                                   int32_t* argmax, int64_t* accepted_slots,
-                                  int64_t* accepted_tokens, int64_t* result,
-                                  uint32_t* counter, void* stream) {
+                                  int64_t* accepted_tokens, int64_t* result, void* workspace,
+                                  void* stream) {
   if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || max_depth < 0)
     return TM_ERR_SHAPE;
   if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
-  const dim3 grid((unsigned)N);
-  if (dtype == TM_DTYPE_F32) {
-    hipLaunchKernelGGL(tm_argmax_walk_kernel<TM_DTYPE_F32>, grid, dim3(kArgThreads), 0,
-                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, tokens,
-                       child_start, child_count, child_list, (int)max_depth, argmax,
-                       accepted_slots, accepted_tokens, result, counter);
-  } else {
-    hipLaunchKernelGGL(tm_argmax_walk_kernel<TM_DTYPE_BF16>, grid, dim3(kArgThreads), 0,
-                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, tokens,
-                       child_start, child_count, child_list, (int)max_depth, argmax,
-                       accepted_slots, accepted_tokens, result, counter);
+  if (((uintptr_t)workspace % 8) != 0) return TM_ERR_ALIGN;
+  const int64_t elem = (dtype == TM_DTYPE_F32) ? 4 : 2;
+  const int64_t width = 16 / elem;  // elements per 16-byte vector
+  // rows are split into `parts` ranges of `per_part` elements (a multiple of
+  // the vector width), about kChunkBytes each, at most TM_OP4_MAX_PARTS
+  int64_t per_part = (kChunkBytes / elem);
+  int64_t parts = (V + per_part - 1) / per_part;
+  if (parts > TM_OP4_MAX_PARTS) {
+    parts = TM_OP4_MAX_PARTS;
+    per_part = ((V + parts - 1) / parts + width - 1) / width * width;
+    parts = (V + per_part - 1) / per_part;
   }
+  const int vec_ok = (((uintptr_t)logits % 16) == 0 && ((row_stride * elem) % 16) == 0) ? 1 : 0;
+  Partial* partial = reinterpret_cast<Partial*>(workspace);
+  const dim3 grid((unsigned)parts, (unsigned)N);
+  if (dtype == TM_DTYPE_F32) {
+    hipLaunchKernelGGL(tm_argmax_part_kernel<TM_DTYPE_F32>, grid, dim3(kArgThreads), 0,
+                       (hipStream_t)stream, logits, (int)V, row_stride, (int)per_part,
+                       (int)parts, vec_ok, partial);
+  } else {
+    hipLaunchKernelGGL(tm_argmax_part_kernel<TM_DTYPE_BF16>, grid, dim3(kArgThreads), 0,
+                       (hipStream_t)stream, logits, (int)V, row_stride, (int)per_part,
+                       (int)parts, vec_ok, partial);
+  }
+  TM_HIP_CHECK_LAUNCH();
+  hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, (hipStream_t)stream,
+                     partial, (int)parts, (int)N, tokens, child_start, child_count, child_list,
+                     (int)max_depth, argmax, accepted_slots, accepted_tokens, result);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }

@@ -3,9 +3,10 @@
 Same call signature as the reference ``fused_verify_commit``
 (treemoe/kernels/op4_commit.py:170-272).  Two launches:
 
-  tm_op4_argmax_walk   first-occurrence argmax of every node's logits and,
-                       in the last workgroup to finish, the greedy accept walk
-                       and the -1-padded result vectors (int64, on device);
+  tm_op4_argmax_walk   first-occurrence argmax of every node's logits (row
+                       ranges over many workgroups), then in one workgroup the
+                       greedy accept walk and the -1-padded result vectors
+                       (int64, on device);
   tm_op4_kv_commit     copy of the K/V rows of [root] + accepted path from the
                        tree scratch pages to positions seq_len, seq_len+1, ...
 
@@ -35,15 +36,9 @@ class VerifyResult:
     num_accepted: torch.Tensor     # [] number of accepted nodes
 
 
-_counters: dict[int, torch.Tensor] = {}
-
-
-def _counter(device: torch.device) -> torch.Tensor:
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    c = _counters.get(idx)
-    if c is None:
-        c = _counters[idx] = torch.zeros(1, dtype=torch.int32, device=device)
-    return c
+def argmax_workspace(n: int, device) -> torch.Tensor:
+    """Scratch of the row-range argmax: N * TM_OP4_MAX_PARTS (value, index) pairs."""
+    return torch.empty(n * _capi.TM_OP4_MAX_PARTS * 8, dtype=torch.uint8, device=device)
 
 
 def _children_csr(children: list[list[int]], n: int, device) -> torch.Tensor:
@@ -101,7 +96,7 @@ def fused_verify_commit(
     stream = _capi.stream_of(dev)
     call("tm_op4_argmax_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
          ptr(tokens), ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n, max_depth, ptr(argmax),
-         ptr(slots), ptr(toks), ptr(result), ptr(_counter(dev)), stream)
+         ptr(slots), ptr(toks), ptr(result), ptr(argmax_workspace(n, dev)), stream)
     res = VerifyResult(accepted_slots=slots, accepted_tokens=toks,
                        bonus_token=result[0], num_accepted=result[1])
     if kv is not None:
