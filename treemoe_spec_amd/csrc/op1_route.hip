@@ -101,18 +101,22 @@ struct BucketArgs {
 };
 
 constexpr int kStageFloats = 16384;  // gates staged in LDS when T * E fits (64 KB)
+constexpr int kMaxBlocks = kMaxPaddedRows / 16;
 
 struct BucketShared {
   float gates[kStageFloats];
   float accept[TM_MAX_TOKENS];
   float demand[TM_MAX_EXPERTS];
   float crit[TM_MAX_EXPERTS];
-  int keep[TM_MAX_EXPERTS];
   int count[TM_MAX_EXPERTS];
   int block_start[TM_MAX_EXPERTS];
   int nblocks[TM_MAX_EXPERTS];
   int offset[TM_MAX_EXPERTS + 1];
-  uint8_t fe[kMaxSlots];
+  unsigned long long keep;              // bit e: expert e is in the budget
+  uint8_t fe[kMaxSlots];                // expert of slot s
+  uint8_t inrank[kMaxSlots];            // rank of slot s among its expert's slots in its chunk
+  uint16_t sorted[kMaxSlots];           // compact expert-major order
+  int16_t owner[kMaxBlocks];            // expert of padded block b, -1 unused
   uint16_t cnt[kMaxChunks * TM_MAX_EXPERTS];
 };
 
@@ -128,6 +132,25 @@ __device__ __forceinline__ int wave_exclusive_scan(int v, int lane, int* total) 
   return inc - v;
 }
 
+// Top-2 in one pass over e = 0, 1, ...: the first pick is the first maximum;
+// the second is the first maximum of the others (a later equal value never
+// displaces an earlier one).
+struct Top2 {
+  int i1, i2;
+  float g1, g2;
+  __device__ __forceinline__ void offer(float v, int e) {
+    if (i1 < 0 || v > g1) {
+      g2 = g1;
+      i2 = i1;
+      g1 = v;
+      i1 = e;
+    } else if (i2 < 0 || v > g2) {
+      g2 = v;
+      i2 = e;
+    }
+  }
+};
+
 // Budget routing and bucketing for all T tokens in one workgroup.
 //
 //  1. demand[e] = sum_t accept[t] * gates[t, e]: lane l of the wave that owns
@@ -137,16 +160,17 @@ __device__ __forceinline__ int wave_exclusive_scan(int v, int lane, int* total) 
 //     the critical-path objective the order is (crit desc, demand desc, e asc)
 //     with crit[e] = max accept over nodes whose unrestricted top-1, or top-2
 //     when accept >= tau, is e (tree_moe_ref.py:35-49, op1_tree_moe.py:195-217).
+//     Expert e is kept when fewer than `budget` experts precede it in that
+//     (strict, total) order.
 //  3. per token: top-2 of the kept gates (ties to the lower expert id, the
 //     second pick excludes the first), weights p_k / (p1 + p2), and (1, 0) when
 //     accept < tau (tree_moe_ref.py:51-66).
 //  4. slot s = 2t + k; stable rank inside its expert from wave ballots and a
-//     scan over 64-slot chunks; the reference's padded BM-row block layout
-//     (op1_tree_moe.py:111-144) and the compact expert-major order with its
-//     GEMM tile list.
-// Gates and accept are staged in LDS first; every serial step is a wave-wide
-// reduction or scan (one lane per expert), so no single thread walks a
-// dependent chain of LDS or global loads.
+//     scan over 64-slot chunks; the compact expert-major order with its GEMM
+//     tile list, and the reference's padded BM-row block layout
+//     (op1_tree_moe.py:111-144) read back from the compact order.
+// Gates and accept are staged in LDS first and every intermediate stays in
+// LDS; global memory is written only with final values, each by one thread.
 __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -160,31 +184,30 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
 
   // 0. stage gates and accept
   if (staged) {
-    for (int i = tid; i < T * E; i += kThreads) sh.gates[i] = a.gates[i];
+    const int n = T * E;
+    int done = 0;
+    if ((reinterpret_cast<uintptr_t>(a.gates) & 15) == 0) {
+      const int n4 = n >> 2;
+      const float4* g4 = reinterpret_cast<const float4*>(a.gates);
+      float4* s4 = reinterpret_cast<float4*>(sh.gates);
+#pragma unroll 8
+      for (int i = tid; i < n4; i += kThreads) s4[i] = g4[i];
+      done = n4 << 2;
+    }
+    for (int i = done + tid; i < n; i += kThreads) sh.gates[i] = a.gates[i];
   }
+#pragma unroll 8
   for (int t = tid; t < T; t += kThreads) sh.accept[t] = a.accept[t];
-  for (int i = tid; i < padded_rows; i += kThreads) a.padded_slots[i] = -1;
   __syncthreads();
   const float* G = staged ? sh.gates : a.gates;
 
   if (critical) {
     for (int t = tid; t < T; t += kThreads) {
       const float* g = G + (size_t)t * E;
-      int u1 = 0;
-      float b1 = g[0];
-      for (int e = 1; e < E; ++e) {
-        const float v = g[e];
-        if (v > b1) { b1 = v; u1 = e; }
-      }
-      int u2 = -1;
-      float b2 = 0.0f;
-      for (int e = 0; e < E; ++e) {
-        if (e == u1) continue;
-        const float v = g[e];
-        if (u2 < 0 || v > b2) { b2 = v; u2 = e; }
-      }
-      sh.fe[2 * t] = (uint8_t)u1;
-      sh.fe[2 * t + 1] = (uint8_t)u2;
+      Top2 r{-1, -1, 0.0f, 0.0f};
+      for (int e = 0; e < E; ++e) r.offer(g[e], e);
+      sh.fe[2 * t] = (uint8_t)r.i1;
+      sh.fe[2 * t + 1] = (uint8_t)r.i2;
     }
     __syncthreads();
   }
@@ -215,78 +238,65 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   }
   __syncthreads();
 
-  // 2. keep set (wave 0, lane = expert): `budget` rounds of a wave-wide argmax
-  //    in the order (crit desc,) demand desc, expert asc.
+  // 2. keep set (wave 0, lane = expert): rank in the order (crit desc,)
+  //    demand desc, expert asc.
   if (wave == 0) {
-    const bool valid = lane < E;
-    const float d = valid ? sh.demand[lane] : 0.0f;
-    const float c = (valid && critical) ? sh.crit[lane] : 0.0f;
-    bool kept = false;
-    for (int r = 0; r < a.budget; ++r) {
-      int av = (valid && !kept) ? 1 : 0;
-      float bc = c, bd = d;
-      int be = lane;
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const int oav = __shfl_xor(av, off);
-        const float oc = __shfl_xor(bc, off);
-        const float od = __shfl_xor(bd, off);
-        const int oe = __shfl_xor(be, off);
-        bool take;
-        if (oav != av) {
-          take = oav != 0;
-        } else if (critical && oc != bc) {
-          take = oc > bc;
-        } else if (od != bd) {
-          take = od > bd;
+    int kept = 0;
+    if (lane < E) {
+      const float d = sh.demand[lane];
+      const float c = critical ? sh.crit[lane] : 0.0f;
+      int rank = 0;
+      for (int f = 0; f < E; ++f) {
+        const float df = sh.demand[f];
+        const float cf = critical ? sh.crit[f] : 0.0f;
+        bool before;
+        if (critical && cf != c) {
+          before = cf > c;
+        } else if (df != d) {
+          before = df > d;
         } else {
-          take = oe < be;
+          before = f < lane;
         }
-        if (take) { av = oav; bc = oc; bd = od; be = oe; }
+        rank += before ? 1 : 0;
       }
-      if (lane == be) kept = true;
+      kept = rank < a.budget ? 1 : 0;
     }
-    if (valid) sh.keep[lane] = kept ? 1 : 0;
+    const unsigned long long m = __ballot(kept != 0);
+    if (lane == 0) sh.keep = m;
   }
   __syncthreads();
 
   // 3. in-budget top-2, renormalisation, low-acceptance degrade
+  const unsigned long long keep = sh.keep;
   for (int t = tid; t < T; t += kThreads) {
     const float* g = G + (size_t)t * E;
-    int i1 = -1;
-    float g1 = 0.0f;
-    for (int e = 0; e < E; ++e) {
-      const float v = sh.keep[e] ? g[e] : 0.0f;
-      if (i1 < 0 || v > g1) { g1 = v; i1 = e; }
-    }
-    int i2 = -1;
-    float g2 = 0.0f;
-    for (int e = 0; e < E; ++e) {
-      if (e == i1) continue;
-      const float v = sh.keep[e] ? g[e] : 0.0f;
-      if (i2 < 0 || v > g2) { g2 = v; i2 = e; }
-    }
-    const float s = g1 + g2;
-    float tg1 = g1 / s;
-    float tg2 = g2 / s;
+    Top2 r{-1, -1, 0.0f, 0.0f};
+    for (int e = 0; e < E; ++e) r.offer(((keep >> e) & 1ull) ? g[e] : 0.0f, e);
+    const float s = r.g1 + r.g2;
+    float tg1 = r.g1 / s;
+    float tg2 = r.g2 / s;
     if (sh.accept[t] < a.tau) { tg1 = 1.0f; tg2 = 0.0f; }
-    a.topk_ids[2 * t] = i1;
-    a.topk_ids[2 * t + 1] = i2;
+    a.topk_ids[2 * t] = r.i1;
+    a.topk_ids[2 * t + 1] = r.i2;
     a.gates_flat[2 * t] = tg1;
     a.gates_flat[2 * t + 1] = tg2;
-    sh.fe[2 * t] = (uint8_t)i1;  // the critical-path use of fe ended at an earlier barrier
-    sh.fe[2 * t + 1] = (uint8_t)i2;
+    sh.fe[2 * t] = (uint8_t)r.i1;  // the critical-path use of fe ended at an earlier barrier
+    sh.fe[2 * t + 1] = (uint8_t)r.i2;
   }
   __syncthreads();
 
-  // 4a. per-chunk expert counts from ballots
+  // 4a. per-chunk expert counts and in-chunk ranks from ballots
   for (int q = wave; q < nchunk; q += kWaves) {
     const int s = q * 64 + lane;
     const int fe = (s < nslot) ? (int)sh.fe[s] : -1;
+    int mycnt = 0, inrank = 0;
     for (int e = 0; e < E; ++e) {
       const unsigned long long m = __ballot(fe == e);
-      if (lane == 0) sh.cnt[q * TM_MAX_EXPERTS + e] = (uint16_t)__popcll(m);
+      if (lane == e) mycnt = __popcll(m);
+      if (fe == e) inrank = __popcll(m & ((1ull << lane) - 1ull));
     }
+    if (lane < E) sh.cnt[q * TM_MAX_EXPERTS + lane] = (uint16_t)mycnt;
+    if (s < nslot) sh.inrank[s] = (uint8_t)inrank;
   }
   __syncthreads();
   // 4b. exclusive scan over chunks (slot order) per expert; chunks q and q+64
@@ -339,24 +349,15 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     }
   }
   __syncthreads();
-  // 4d. stable in-expert rank -> destinations
-  for (int q = wave; q < nchunk; q += kWaves) {
-    const int s = q * 64 + lane;
-    const int fe = (s < nslot) ? (int)sh.fe[s] : -1;
-    int inrank = 0;
-    for (int e = 0; e < E; ++e) {
-      const unsigned long long m = __ballot(fe == e);
-      if (fe == e) inrank = __popcll(m & ((1ull << lane) - 1ull));
-    }
-    if (s < nslot) {
-      const int rank = (int)sh.cnt[q * TM_MAX_EXPERTS + fe] + inrank;
-      const int dest = sh.block_start[fe] * a.BM + rank;
-      const int pos = sh.offset[fe] + rank;
-      a.slot_to_row[s] = dest;
-      if (dest < padded_rows) a.padded_slots[dest] = s;
-      a.sorted_slots[pos] = s;
-      a.slot_pos[s] = pos;
-    }
+  // 4d. destinations of every slot, and the owner of every padded block
+  for (int s = tid; s < nslot; s += kThreads) {
+    const int fe = sh.fe[s];
+    const int rank = (int)sh.cnt[(s >> 6) * TM_MAX_EXPERTS + fe] + (int)sh.inrank[s];
+    const int pos = sh.offset[fe] + rank;
+    a.slot_to_row[s] = sh.block_start[fe] * a.BM + rank;
+    a.sorted_slots[pos] = s;
+    a.slot_pos[s] = pos;
+    sh.sorted[pos] = (uint16_t)s;
   }
   for (int b = tid; b < a.max_blocks; b += kThreads) {
     int owner = -1;
@@ -364,7 +365,20 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
       if (sh.nblocks[e] > 0 && b >= sh.block_start[e] && b < sh.block_start[e] + sh.nblocks[e])
         owner = e;
     }
+    sh.owner[b] = (int16_t)owner;
     a.block_expert_ids[b] = owner;
+  }
+  __syncthreads();
+  // 4e. padded rows: row i of block b holds the (i - first row of the owner)-th
+  //     slot of the owning expert, or -1 past its count or in an unused block.
+  for (int i = tid; i < padded_rows; i += kThreads) {
+    const int e = sh.owner[i / a.BM];
+    int64_t slot = -1;
+    if (e >= 0) {
+      const int rank = i - sh.block_start[e] * a.BM;
+      if (rank < sh.count[e]) slot = sh.sorted[sh.offset[e] + rank];
+    }
+    a.padded_slots[i] = slot;
   }
 }
 
@@ -376,7 +390,7 @@ tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg
 }
 
 __global__ void __launch_bounds__(kThreads) tm_bucket_kernel(BucketArgs args) {
-  __shared__ BucketShared sh;
+  __shared__ __attribute__((aligned(16))) BucketShared sh;
   bucket_all(args, sh);
 }
 
