@@ -115,12 +115,11 @@ template <int NSUB>
 __device__ __forceinline__ void gemm1_item(uint8_t* lds, const uint16_t* x, const uint16_t* w1,
                                            const uint16_t* w3, uint16_t* __restrict__ hsw,
                                            const int32_t* __restrict__ sorted_slots, int tile,
-                                           int e, int row0, int rows, int H, int I,
+                                           int ng, int e, int row0, int rows, int H, int I,
                                            uint32_t x_bytes) {
   using C = Cfg<NSUB>;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
-  const int ng = blockIdx.x;
   uint8_t* scratch = lds + wave * 2 * ROWS * C::SROW;
 
   WeightRows<NSUB> wr1, wr3;
@@ -228,18 +227,30 @@ __global__ void __launch_bounds__(256, 2)
 tm_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
                 const uint16_t* __restrict__ w3, uint16_t* __restrict__ hsw,
                 const int32_t* __restrict__ sorted_slots, const int32_t* __restrict__ tiles,
-                int H, int I, uint32_t x_bytes) {
+                int max_tiles, int H, int I, uint32_t x_bytes, int group_major) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kScratchBytes];
-  const int tile = blockIdx.y;
+  // Job order.  Group-major (weight group ng major, tile minor): consecutive
+  // workgroups stream the same rows of different experts' weights, measured
+  // 4-5 % faster at T = 64 (one tile per expert).  Tile-major when experts
+  // have many tiles: consecutive workgroups then share one tile's x rows.
+  const int gpt = I / ROWS;
+  int ng, tile;
+  if (group_major) {
+    ng = (int)blockIdx.x / max_tiles;
+    tile = (int)blockIdx.x - ng * max_tiles;
+  } else {
+    tile = (int)blockIdx.x / gpt;
+    ng = (int)blockIdx.x - tile * gpt;
+  }
   const int e = tiles[4 * tile];
   if (e < 0) return;
   const int row0 = tiles[4 * tile + 1];
   const int rows = tiles[4 * tile + 2];
   switch ((rows + 15) >> 4) {
-    case 1: gemm1_item<1>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
-    case 2: gemm1_item<2>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
-    case 3: gemm1_item<3>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
-    default: gemm1_item<4>(lds, x, w1, w3, hsw, sorted_slots, tile, e, row0, rows, H, I, x_bytes); break;
+    case 1: gemm1_item<1>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
+    case 2: gemm1_item<2>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
+    case 3: gemm1_item<3>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
+    default: gemm1_item<4>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
   }
 }
 
@@ -421,11 +432,12 @@ extern "C" int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void*
       max_tiles * MT * I * 2 >= (int64_t)kOutOfRange)
     return TM_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(w1) || !aligned16(w3) || !aligned16(h)) return TM_ERR_ALIGN;
-  const dim3 grid((unsigned)(I / ROWS), (unsigned)max_tiles);
+  if ((I / ROWS) * max_tiles > INT32_MAX) return TM_ERR_SHAPE;
+  const dim3 grid((unsigned)((I / ROWS) * max_tiles));
   hipLaunchKernelGGL(tm_gemm1_kernel, grid, dim3(64 * WAVES), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)w1, (const uint16_t*)w3,
-                     (uint16_t*)h, sorted_slots, tiles, (int)H, (int)I,
-                     (uint32_t)(T * H * 2));
+                     (uint16_t*)h, sorted_slots, tiles, (int)max_tiles, (int)H, (int)I,
+                     (uint32_t)(T * H * 2), max_tiles <= 2 * E ? 1 : 0);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
