@@ -22,8 +22,8 @@ def declared_functions() -> list[str]:
 def test_header_declares_entry_points():
     names = declared_functions()
     for n in ("tm_version", "tm_status_string", "tm_op1_router_gates", "tm_op1_route_bucket",
-              "tm_op1_gemm1", "tm_op1_gemm2", "tm_op1_combine", "tm_op4_argmax_walk",
-              "tm_op4_kv_commit"):
+              "tm_op1_gemm1", "tm_op1_gemm2", "tm_op1_combine", "tm_op1_prefill_gemm1",
+              "tm_op1_prefill_gemm2", "tm_op4_argmax_walk", "tm_op4_kv_commit"):
         assert n in names
 
 
@@ -54,6 +54,11 @@ def test_status_strings():
     (("tm_op1_gemm1", 0, 0, 0, 0, 0, 0, 1, 64, 4000, 14336, 8, 0), 1001),  # H % 256
     (("tm_op1_gemm2", 0, 0, 0, 0, 0, 0, 1, 3, 64, 4096, 14336, 8, 0), 1001),  # split
     (("tm_op1_combine", 0, 0, 0, 64, 4094, 2, 0), 1001),
+    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4000, 14336, 8, 0), 1001),  # H % 64
+    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 0, 2048, 4096, 14336, 8, 0), 1001),  # tiles
+    (("tm_op1_prefill_gemm1", 8, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14336, 8, 0), 1002),  # align
+    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 2, 2048, 4032, 14336, 8, 0), 1001),  # H % 128
+    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 3, 2048, 4096, 14336, 8, 0), 1001),  # split
     (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1003),
     (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1001),
 ])

@@ -304,6 +304,79 @@ def test_exclude_experts_hybrid_matches_full():
     torch.testing.assert_close(hybrid, full.float().cpu(), rtol=2e-2, atol=5e-2)
 
 
+@pytest.mark.parametrize("t,budget,objective", [(512, 8, "mass"), (512, 2, "critical_path"),
+                                                (300, 4, "mass"), (1024, 3, "critical_path")])
+def test_tiled_gemms_match_fp64_golden(t, budget, objective):
+    """At >= 128 rows per routed expert the MFMA-tiled GEMMs run; expert row
+    counts that are not multiples of 128 (and unrouted experts) included."""
+    _say(f"tiled t={t} B={budget} {objective}")
+    m = _op1()
+    assert m.uses_tiled_gemms(t, budget, 8)
+    out, golden, _, _ = _forward_and_golden(t, 8, 512, 1024, budget, 31 + t, objective)
+    err = op1_ref.rel_l2(out.cpu().float(), golden)
+    _say(f"  rel_l2={err:.3e}")
+    assert err <= REL_L2_TOL
+
+
+def test_tiled_gemms_skewed_expert():
+    """One expert takes every token (several 128-row tiles plus a ragged one)."""
+    _say("tiled skewed")
+    m = _op1()
+    t, e, h, i = 700, 8, 512, 1024
+    g = torch.Generator().manual_seed(41)
+    x, w1, w2, w3, router, accept = make_moe_inputs(t, e, h, i, g, dtype=torch.float32)
+    x[:, 0] = 1.0
+    router[:, 0] = 0.0
+    router[5, 0] = 40.0
+    args = [a.to(torch.bfloat16) for a in (x, w1, w2, w3, router)]
+    dev = [a.cuda() for a in args] + [accept.cuda()]
+    out = m.tree_moe_forward(*dev, 8)
+    gates = oracle_c.router_gates(bf16_bits(args[0]), bf16_bits(args[4]))
+    ref = oracle_c.route_bucket(gates, accept.numpy(), 8)
+    assert np.sum(ref.topk_ids == 5) == t
+    golden = op1_ref.expert_ffn_golden(args[0], args[1], args[2], args[3],
+                                       torch.from_numpy(ref.topk_ids).view(t, 2),
+                                       torch.from_numpy(ref.gates_flat).view(t, 2))
+    assert op1_ref.rel_l2(out.cpu().float(), golden) <= REL_L2_TOL
+
+
+def test_tiled_and_streaming_gemms_agree(monkeypatch):
+    _say("tiled vs streaming")
+    m = _op1()
+    g = torch.Generator().manual_seed(43)
+    x, w1, w2, w3, router, accept = make_moe_inputs(512, 8, 1024, 2048, g, dtype=torch.bfloat16)
+    dev = [a.cuda() for a in (x, w1, w2, w3, router, accept)]
+    assert m.uses_tiled_gemms(512, 8, 8)
+    tiled = m.tree_moe_forward(*dev, 8).clone()
+    again = m.tree_moe_forward(*dev, 8)
+    assert torch.equal(tiled, again)
+    monkeypatch.setattr(m, "TILED_MIN_ROWS", 1 << 30)
+    assert not m.uses_tiled_gemms(512, 8, 8)
+    streaming = m.tree_moe_forward(*dev, 8)
+    assert op1_ref.rel_l2(tiled.float().cpu(), streaming.float().cpu()) <= 5e-3
+
+
+def test_exclude_experts_tiled_path():
+    _say("exclude experts, tiled")
+    m = _op1()
+    t, budget = 512, 4
+    g = torch.Generator().manual_seed(47)
+    x, w1, w2, w3, router, accept = make_moe_inputs(t, 8, 512, 1024, g, dtype=torch.bfloat16)
+    dev = [a.cuda() for a in (x, w1, w2, w3, router, accept)]
+    assert m.uses_tiled_gemms(t, budget, 8)
+    full = m.tree_moe_forward(*dev, budget).clone()
+    routing = m.route_experts(dev[0], dev[4], dev[5], budget, 1024)
+    cold = routing.expert_ids()[:2]
+    info = routing.exclude_experts(cold)
+    hybrid = m.tree_moe_forward(*dev, budget, routing=routing).float().cpu()
+    for e, toks, gts in info:
+        xe = x[toks].double()
+        y = (torch.nn.functional.silu(xe @ w1[e].double().t()) * (xe @ w3[e].double().t())) \
+            @ w2[e].double().t()
+        hybrid.index_add_(0, toks, (gts.double().unsqueeze(1) * y).float())
+    torch.testing.assert_close(hybrid, full.float().cpu(), rtol=2e-2, atol=5e-2)
+
+
 def _torch_fp32_golden(inp, ids, wts):
     """Same expert FFN in fp32 torch on the GPU (hipBLASLt), for full shapes."""
     x = inp.x.float()

@@ -26,6 +26,8 @@ SIGNATURES: dict[str, list] = {
     "tm_op1_gemm1": [P, P, P, P, P, P, I64, I64, I64, I64, I64, P],
     "tm_op1_gemm2": [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
     "tm_op1_combine": [P, P, P, I64, I64, I64, P],
+    "tm_op1_prefill_gemm1": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P],
+    "tm_op1_prefill_gemm2": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
     "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P, P, P, P],
     "tm_op4_kv_commit": [P, P, I64, I64, I64, I64, I64, I64, I64, P, P, P, I64, P, I64, I64,
                          I64, P],

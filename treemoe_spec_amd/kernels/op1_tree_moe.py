@@ -47,6 +47,17 @@ def compact_block_capacity(num_slots: int, expert_budget: int, block_m: int = BM
     return 1 << max(logical - 1, 0).bit_length()
 
 
+# Rows per active expert from which the MFMA-tiled GEMMs (128-row tiles that
+# reuse each weight tile across rows) replace the weight-streaming GEMMs
+# (one pass over an expert's weights per 64-row tile).
+TILED_MIN_ROWS = 128
+
+
+def uses_tiled_gemms(num_tokens: int, expert_budget: int, num_experts: int) -> bool:
+    """True when the average rows per routed expert reach TILED_MIN_ROWS."""
+    return 2 * num_tokens >= TILED_MIN_ROWS * min(expert_budget, num_experts)
+
+
 def _split_for(inter: int) -> int:
     for s in (SPLIT_K, 2, 1):
         if s >= 1 and inter % s == 0 and (inter // s) % 256 == 0:
@@ -345,11 +356,19 @@ def tree_moe_forward(
             or routing.max_tiles > ws.max_tiles):
         raise ValueError("routing was computed for a different shape")
     stream = _capi.stream_of(x.device)
-    call("tm_op1_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h), ptr(routing.sorted_slots),
-         ptr(routing.tiles), routing.max_tiles, n, hidden, inter, e, stream)
-    call("tm_op1_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial), ptr(routing.gates_flat),
-         ptr(routing.sorted_slots), ptr(routing.tiles), routing.max_tiles, ws.split, n,
-         hidden, inter, e, stream)
+    if uses_tiled_gemms(n, expert_budget, e):
+        call("tm_op1_prefill_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h),
+             ptr(routing.sorted_slots), ptr(routing.expert_offsets), ptr(routing.tiles),
+             routing.max_tiles, n, hidden, inter, e, stream)
+        call("tm_op1_prefill_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial),
+             ptr(routing.gates_flat), ptr(routing.sorted_slots), ptr(routing.expert_offsets),
+             ptr(routing.tiles), routing.max_tiles, ws.split, n, hidden, inter, e, stream)
+    else:
+        call("tm_op1_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h), ptr(routing.sorted_slots),
+             ptr(routing.tiles), routing.max_tiles, n, hidden, inter, e, stream)
+        call("tm_op1_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial), ptr(routing.gates_flat),
+             ptr(routing.sorted_slots), ptr(routing.tiles), routing.max_tiles, ws.split, n,
+             hidden, inter, e, stream)
     if out is not None:
         if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
             raise ValueError("out must be a contiguous tensor like x")
