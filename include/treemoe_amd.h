@@ -210,6 +210,44 @@ int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
                        void* workspace, void* stream);
 
 /*
+ * Repetition penalty, in place on every row of logits [N, V] (row stride
+ * `row_stride`, TM_DTYPE_F32 or TM_DTYPE_BF16).  Replaces pass 0 of
+ * `_postprocess_softmax_kernel` (treemoe/kernels/op4_commit.py:53-57) as
+ * launched for greedy verification with rep_penalty != 1 (:201-214): for each
+ * of the num_prev tokens in order, x = x > 0 ? x / penalty : x * penalty, so a
+ * token listed k times is penalised k times (bf16 rows are rounded after each
+ * application, as the reference stores them).  Tokens outside [0, V) are
+ * skipped.  `table`: 2 * table_size int32 of device memory, table_size a power
+ * of two >= 2 * num_prev; no initial contents required.
+ */
+int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V, int64_t row_stride,
+                       const int64_t* prev_tokens, int64_t num_prev, float penalty,
+                       int32_t* table, int64_t table_size, void* stream);
+
+/*
+ * Tree rejection sampling walk (temperature > 0), one launch.  Replaces the
+ * sampling branch of `tree_verify_ref` (treemoe/ref/verify_ref.py:60-89), which
+ * the reference's fused_verify_commit runs for temperature > 0
+ * (treemoe/kernels/op4_commit.py:187-196).  At the current node the residual
+ * is softmax(logits[node] / temperature); children are tried in child-list
+ * order, child c (token t) is accepted when
+ *   uniforms[c] < min(residual[t] / max(q_c[t], 1e-20), 1),  q_c = draft_probs[c],
+ * and otherwise residual = max(residual - q_c, 0) / max(sum, 1e-20).  Depth is
+ * unbounded (at most N accepted nodes).  When every child is rejected (or at a
+ * leaf) the bonus token is the smallest j with residual[0] + .. + residual[j] >
+ * bonus_u[0] * sum (inverse CDF; the reference calls torch.multinomial).
+ * draft_probs: [N, V] fp32, row stride q_stride.  uniforms [N], bonus_u [1]
+ * fp32 on the device.  residual: V fp32 of device memory.  Outputs as
+ * tm_op4_argmax_walk.
+ */
+int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int64_t V, int64_t row_stride,
+                       const float* draft_probs, int64_t q_stride, const int64_t* tokens,
+                       const int32_t* child_start, const int32_t* child_count,
+                       const int32_t* child_list, const float* uniforms, const float* bonus_u,
+                       float temperature, float* residual, int64_t* accepted_slots,
+                       int64_t* accepted_tokens, int64_t* result, void* stream);
+
+/*
  * Paged KV commit of [root] + accepted path.  Replaces `_kv_commit_kernel` and
  * its host glue (treemoe/kernels/op4_commit.py:134-167, 241-267); reference
  * semantics `PagedKVCache.commit_tree` (treemoe/model/kv_cache.py:88-106).

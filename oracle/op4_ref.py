@@ -16,8 +16,12 @@ import torch
 def tree_verify(target_logits: torch.Tensor, draft_probs: torch.Tensor,
                 tree_tokens: torch.Tensor, children: list[list[int]],
                 temperature: float = 0.0, uniforms: torch.Tensor | None = None,
-                generator: torch.Generator | None = None):
-    """Returns (accepted_slots [N], accepted_tokens [N], bonus, num_accepted)."""
+                generator: torch.Generator | None = None,
+                bonus_uniform: float | None = None, return_residual: bool = False):
+    """Returns (accepted_slots [N], accepted_tokens [N], bonus, num_accepted)
+    (+ the final residual when return_residual).  With bonus_uniform the
+    sampling-mode bonus is the inverse-CDF draw ``inverse_cdf(residual, u)``
+    instead of torch.multinomial."""
     n = target_logits.shape[0]
     slots: list[int] = []
     toks: list[int] = []
@@ -48,6 +52,8 @@ def tree_verify(target_logits: torch.Tensor, draft_probs: torch.Tensor,
         if taken < 0:
             if temperature == 0.0:
                 bonus = best
+            elif bonus_uniform is not None:
+                bonus = inverse_cdf(residual, bonus_uniform)
             else:
                 bonus = int(torch.multinomial(residual, 1, generator=generator))
             break
@@ -59,7 +65,36 @@ def tree_verify(target_logits: torch.Tensor, draft_probs: torch.Tensor,
     if slots:
         acc_slots[: len(slots)] = torch.tensor(slots)
         acc_toks[: len(toks)] = torch.tensor(toks)
+    if return_residual:
+        return acc_slots, acc_toks, bonus, len(slots), residual
     return acc_slots, acc_toks, bonus, len(slots)
+
+
+def inverse_cdf(probs: torch.Tensor, u: float) -> int:
+    """Smallest j with probs[0] + .. + probs[j] > u * sum(probs), in float64
+    (the last positive entry when rounding leaves no such j)."""
+    p = probs.double()
+    c = torch.cumsum(p, 0)
+    target = u * float(c[-1])
+    idx = int(torch.searchsorted(c, torch.tensor([target], dtype=torch.float64), right=True))
+    if idx >= p.numel():
+        nz = (p > 0).nonzero().flatten()
+        idx = int(nz[-1]) if nz.numel() else 0
+    return idx
+
+
+def rep_penalty_inplace(logits: torch.Tensor, prev_tokens, penalty: float) -> None:
+    """Reference `_postprocess_softmax_kernel` pass 0
+    (treemoe/kernels/op4_commit.py:53-57) on every row: for each prev token in
+    order, x = x / penalty if x > 0 else x * penalty, each time loaded from and
+    stored to the tensor (so bf16 rows round after every application)."""
+    v = logits.shape[1]
+    for t in [int(t) for t in prev_tokens]:
+        if t < 0 or t >= v:
+            continue
+        col = logits[:, t].float()
+        col = torch.where(col > 0, col / penalty, col * penalty)
+        logits[:, t] = col.to(logits.dtype)
 
 
 def commit_tree(k: torch.Tensor, v: torch.Tensor, commit_slots: torch.Tensor,

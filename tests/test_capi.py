@@ -23,7 +23,8 @@ def test_header_declares_entry_points():
     names = declared_functions()
     for n in ("tm_version", "tm_status_string", "tm_op1_router_gates", "tm_op1_route_bucket",
               "tm_op1_gemm1", "tm_op1_gemm2", "tm_op1_combine", "tm_op1_prefill_gemm1",
-              "tm_op1_prefill_gemm2", "tm_op4_argmax_walk", "tm_op4_kv_commit"):
+              "tm_op1_prefill_gemm2", "tm_op4_argmax_walk", "tm_op4_rep_penalty",
+              "tm_op4_sample_walk", "tm_op4_kv_commit"):
         assert n in names
 
 
@@ -61,6 +62,15 @@ def test_status_strings():
     (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 3, 2048, 4096, 14336, 8, 0), 1001),  # split
     (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1003),
     (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1001),
+    (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 0, 1.5, 0, 16, 0), 1001),     # no tokens
+    (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 1.5, 0, 12, 0), 1001),     # table size
+    (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 1.5, 0, 4, 0), 1001),      # table < 2n
+    (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 0.0, 0, 16, 0), 1003),     # penalty
+    (("tm_op4_rep_penalty", 0, 5, 4, 10, 10, 0, 4, 1.5, 0, 16, 0), 1003),     # dtype
+    (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 10, 0, 0, 0, 0, 0, 0, 0.0, 0, 0, 0, 0, 0),
+     1003),                                                                     # temperature
+    (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 9, 0, 0, 0, 0, 0, 0, 1.0, 0, 0, 0, 0, 0),
+     1001),                                                                     # q stride
 ])
 def test_argument_errors_return_before_launch(call, expect):
     from treemoe_spec_amd import _capi

@@ -237,12 +237,253 @@ def test_config4_planted_path_accepted():
         assert res.accepted_slots[: len(w.planted_path)].tolist() == w.planted_path
 
 
-def test_rejects_sampling_mode_and_cpu():
+def test_rejects_cpu_and_bad_sampling_inputs():
     op4 = _op4()
     logits = torch.zeros(2, 8)
     with pytest.raises(RuntimeError, match="ROCm"):
         op4.fused_verify_commit(logits, None, torch.zeros(2, dtype=torch.long), None,
                                 [[1], []])
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="draft_probs"):
         op4.fused_verify_commit(logits.cuda(), None, torch.zeros(2, dtype=torch.long), None,
                                 [[1], []], temperature=1.0)
+    with pytest.raises(ValueError, match="draft_probs"):
+        op4.fused_verify_commit(logits.cuda(), torch.zeros(2, 7, device="cuda"),
+                                torch.zeros(2, dtype=torch.long), None, [[1], []],
+                                temperature=1.0)
+
+
+# ------------------------------------------------------------- sampling --
+
+def _dt(t):
+    from treemoe_spec_amd import _capi
+
+    return _capi.TM_DTYPE_F32 if t.dtype == torch.float32 else _capi.TM_DTYPE_BF16
+
+
+def _direct_sample(logits, q, tokens, children, uniforms, bonus_u, temperature):
+    """tm_op4_sample_walk on device tensors; returns (slots, toks, result, residual)."""
+    from treemoe_spec_amd import _capi
+    from treemoe_spec_amd.kernels.op4_commit import _children_csr
+
+    n, v = logits.shape
+    assert q.shape == (n, v) and tokens.numel() == n and uniforms.numel() >= n
+    csr = _children_csr(children, n, "cuda")
+    slots = torch.empty(n, dtype=torch.int64, device="cuda")
+    toks = torch.empty(n, dtype=torch.int64, device="cuda")
+    result = torch.empty(3, dtype=torch.int64, device="cuda")
+    residual = torch.empty(v, dtype=torch.float32, device="cuda")
+    p = _capi.ptr
+    _capi.call("tm_op4_sample_walk", p(logits), _dt(logits), n, v, logits.stride(0), p(q),
+               q.stride(0), p(tokens), p(csr), p(csr) + 4 * n, p(csr) + 8 * n, p(uniforms),
+               p(bonus_u), float(temperature), p(residual), p(slots), p(toks), p(result),
+               _capi.stream_of(logits.device))
+    torch.cuda.synchronize()
+    return slots.cpu(), toks.cpu(), result.cpu(), residual.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_sampling_injected_uniforms_kat(dtype):
+    """Reference tests/test_op4.py:54-67: u = 0 accepts the whole chain,
+    u = 1 rejects the first child."""
+    _say(f"sampling KAT {dtype}")
+    tokens = torch.tensor([5, 7, 9]).cuda()
+    children = [[1], [2], []]
+    logits = torch.zeros(3, 32)
+    for i, w in enumerate([7, 9, 11]):
+        logits[i, w] = 10.0
+    logits = logits.to(dtype).cuda()
+    q = torch.full((3, 32), 1.0 / 32, device="cuda")
+    bu = torch.full((1,), 0.5, device="cuda")
+    slots, toks, result, _ = _direct_sample(logits, q, tokens, children,
+                                            torch.zeros(3, device="cuda"), bu, 1.0)
+    assert int(result[1]) == 2 and slots.tolist() == [1, 2, -1] and toks.tolist() == [7, 9, -1]
+    assert int(result[2]) == 2
+    slots, toks, result, _ = _direct_sample(logits, q, tokens, children,
+                                            torch.ones(3, device="cuda"), bu, 1.0)
+    assert int(result[1]) == 0 and slots.tolist() == [-1, -1, -1]
+    assert int(result[2]) == 0
+
+
+def _sampling_case(seed, n, v, follow):
+    """Random tree whose child tokens follow the parent's most likely token
+    with probability `follow`, and per-node draft distributions."""
+    g, parent, children, tokens, _ = _tree(seed, n, v)
+    logits = torch.randn(n, v, generator=g) * 3
+    q = torch.softmax(torch.randn(n, v, generator=g) * 2, -1)
+    for node, kids in enumerate(children):
+        if kids and float(torch.rand(1, generator=g)) < follow:
+            tokens[kids[int(torch.randint(0, len(kids), (1,), generator=g))]] = \
+                int(logits[node].argmax())
+    return g, children, tokens, logits, q
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("seed,n,v,temperature", [
+    (1, 16, 64, 1.0), (2, 64, 32000, 0.7), (3, 33, 1000, 1.5), (4, 64, 32001, 1.0),
+    (5, 8, 5, 0.3), (6, 64, 4096, 2.0)])
+def test_sampling_matches_oracle(dtype, seed, n, v, temperature):
+    """Accept path, next root and bonus bit-exact against the oracle with the
+    same uniforms; the final residual within rtol 1e-4 / atol 1e-6 (fp32
+    softmax and residual updates with a different exp and summation order).
+    bf16 logits: the oracle gets them widened to fp32, as the kernel reads them."""
+    _say(f"sampling seed={seed} n={n} v={v} T={temperature} {dtype}")
+    for rep in range(4):
+        g, children, tokens, logits, q = _sampling_case(seed * 10 + rep, n, v, 0.8)
+        logits = logits.to(dtype)
+        u = torch.rand(n, generator=g)
+        bu = float(torch.rand(1, generator=g))
+        slots, toks, result, residual = _direct_sample(
+            logits.cuda(), q.cuda(), tokens.cuda(), children, u.cuda(),
+            torch.tensor([bu], device="cuda"), temperature)
+        r_slots, r_toks, r_bonus, r_num, r_res = op4_ref.tree_verify(
+            logits.float(), q, tokens, children, temperature=temperature, uniforms=u,
+            bonus_uniform=bu, return_residual=True)
+        assert int(result[1]) == r_num
+        assert torch.equal(slots, r_slots) and torch.equal(toks, r_toks)
+        assert int(result[2]) == (int(r_slots[r_num - 1]) if r_num else 0)
+        torch.testing.assert_close(residual, r_res.float(), rtol=1e-4, atol=1e-6)
+        assert int(result[0]) == r_bonus
+
+
+def test_sampling_first_token_distribution():
+    """The emitted first token (accepted child or bonus) is distributed as
+    p = softmax(logits[root] / T) when child tokens are drawn from their draft
+    distributions: 4000 launches, 6-sigma binomial bound per token."""
+    _say("sampling distribution")
+    v, temperature, trials = 6, 0.8, 4000
+    g = torch.Generator().manual_seed(21)
+    logits = (torch.randn(4, v, generator=g) * 1.5).cuda()
+    q = torch.softmax(torch.randn(4, v, generator=g) * 1.5, -1)
+    children = [[1, 2, 3], [], [], []]
+    p = torch.softmax(logits[0].cpu() / temperature, -1).double().numpy()
+    tokens = torch.zeros(trials, 4, dtype=torch.long)
+    for c in (1, 2, 3):
+        tokens[:, c] = torch.multinomial(q[c], trials, replacement=True, generator=g)
+    tokens = tokens.cuda()
+    u = torch.rand(trials, 4, generator=g).cuda()
+    bu = torch.rand(trials, generator=g).cuda()
+    q = q.cuda()
+    from treemoe_spec_amd import _capi
+    from treemoe_spec_amd.kernels.op4_commit import _children_csr
+
+    csr = _children_csr(children, 4, "cuda")
+    slots = torch.empty(trials, 4, dtype=torch.int64, device="cuda")
+    toks = torch.empty(trials, 4, dtype=torch.int64, device="cuda")
+    result = torch.empty(trials, 3, dtype=torch.int64, device="cuda")
+    residual = torch.empty(v, dtype=torch.float32, device="cuda")
+    P = _capi.ptr
+    stream = _capi.stream_of(logits.device)
+    for t in range(trials):
+        _capi.call("tm_op4_sample_walk", P(logits), _dt(logits), 4, v, v, P(q), v,
+                   P(tokens[t]), P(csr), P(csr) + 16, P(csr) + 32, P(u[t]), P(bu[t]),
+                   temperature, P(residual), P(slots[t]), P(toks[t]), P(result[t]), stream)
+    torch.cuda.synchronize()
+    num = result[:, 1].cpu()
+    first = torch.where(num > 0, toks[:, 0].cpu(), result[:, 0].cpu())
+    counts = np.bincount(first.numpy(), minlength=v)
+    sigma = np.sqrt(trials * p * (1 - p))
+    assert np.all(np.abs(counts - trials * p) <= 6 * sigma), (counts, trials * p)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_sampling_draws_from_the_generator_and_commits(dtype):
+    """fused_verify_commit(temperature > 0) draws N accept uniforms then one
+    bonus uniform from the caller's generator on the logits' device; the
+    commit moves [root] + accepted path, bytes equal to the oracle."""
+    _say(f"fused sampling + commit {dtype}")
+    op4 = _op4()
+    n, v, seq_len, page = 64, 4096, 37, 16
+    g, children, tokens, logits, q = _sampling_case(77, n, v, 0.9)
+    logits = logits.to(dtype).cuda()
+    kv = _kv_setup(4, 2, 8, page, 40, seq_len, n, 9, torch.bfloat16)
+    k0, v0 = kv.k.cpu(), kv.v.cpu()
+    gen = torch.Generator(device="cuda").manual_seed(1234)
+    res = op4.fused_verify_commit(logits, q.cuda(), tokens.cuda(), None, children, kv=kv,
+                                  temperature=0.9, generator=gen)
+    torch.cuda.synchronize()
+    gen2 = torch.Generator(device="cuda").manual_seed(1234)
+    u = torch.rand(n, generator=gen2, device="cuda").cpu()
+    bu = float(torch.rand(1, generator=gen2, device="cuda"))
+    r_slots, r_toks, r_bonus, r_num = op4_ref.tree_verify(
+        logits.float().cpu(), q, tokens, children, temperature=0.9, uniforms=u,
+        bonus_uniform=bu)
+    assert int(res.num_accepted) == r_num and int(res.bonus_token) == r_bonus
+    assert torch.equal(res.accepted_slots.cpu(), r_slots)
+    assert torch.equal(res.accepted_tokens.cpu(), r_toks)
+    assert kv.seq_len == seq_len + r_num + 1
+    commit = torch.cat([torch.zeros(1, dtype=torch.long), r_slots])
+    assert op4_ref.commit_tree(k0, v0, commit, kv.tree_pages, kv.block_table, seq_len) == r_num + 1
+    assert torch.equal(kv.k.cpu(), k0) and torch.equal(kv.v.cpu(), v0)
+
+
+# ---------------------------------------------------------- rep penalty --
+
+def _direct_penalty(logits, prev, penalty):
+    from treemoe_spec_amd import _capi
+    from treemoe_spec_amd.kernels.op4_commit import _penalty_table_size
+
+    n, v = logits.shape
+    size = _penalty_table_size(prev.numel())
+    table = torch.empty(2 * size, dtype=torch.int32, device="cuda")
+    p = _capi.ptr
+    _capi.call("tm_op4_rep_penalty", p(logits), _dt(logits), n, v, logits.stride(0), p(prev),
+               prev.numel(), float(penalty), p(table), size, _capi.stream_of(logits.device))
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,v,num_prev,penalty", [
+    (16, 32000, 40, 1.3), (64, 32000, 5000, 1.1), (3, 7, 12, 0.7), (5, 1000, 1, 2.5)])
+def test_rep_penalty_matches_oracle(dtype, n, v, num_prev, penalty):
+    """Bit-exact against the oracle: duplicates applied once per listing,
+    out-of-range entries skipped, bf16 rounded after every application,
+    rows addressed through a row stride wider than V."""
+    _say(f"rep penalty {dtype} n={n} v={v} prev={num_prev} p={penalty}")
+    g = torch.Generator().manual_seed(n + v + num_prev)
+    base = (torch.randn(n, v + 3, generator=g) * 4).to(dtype)
+    base[:, ::5] = -base[:, ::5].abs()
+    base[:, 1] = 0.0
+    prev = torch.randint(0, v, (num_prev,), generator=g)
+    if num_prev > 4:
+        prev[:4] = torch.tensor([-1, v, int(prev[5]), int(prev[5])])
+    got = base.cuda()
+    _direct_penalty(got[:, :v], prev.cuda(), penalty)
+    want = base.clone()
+    op4_ref.rep_penalty_inplace(want[:, :v], prev, penalty)
+    assert torch.equal(got.cpu(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_with_rep_penalty(dtype):
+    """fused_verify_commit(rep_penalty != 1): logits penalised in place like the
+    reference, then the greedy walk over them; a penalised argmax flips the
+    accept decision; no prev_tokens penalises token 0 once."""
+    _say(f"greedy + rep penalty {dtype}")
+    op4 = _op4()
+    n, v = 8, 512
+    tokens = torch.tensor([3, 10, 11, 12, 13, 14, 15, 16])
+    children = [[1, 2], [3], [], [4], [], [], [], []]
+    logits = torch.randn(n, v, generator=torch.Generator().manual_seed(9))
+    logits[0, 10], logits[0, 11] = 9.0, 8.0     # 10 wins unless penalised
+    logits[1, 12] = 9.0
+    logits[3, 13] = 9.0
+    logits[4, 0] = 20.0                         # still row 4's argmax once penalised
+    logits = logits.to(dtype)
+    prev = torch.tensor([10, 10, 7])
+    for prev_arg, penalty in ((prev, 1.5), (None, 1.5), (prev, 1.0)):
+        lg = logits.clone().cuda()
+        res = op4.fused_verify_commit(lg, None, tokens.cuda(), None, children,
+                                      rep_penalty=penalty, prev_tokens=prev_arg)
+        want = logits.clone()
+        if penalty != 1.0:
+            op4_ref.rep_penalty_inplace(want, prev_arg if prev_arg is not None
+                                        else torch.zeros(1, dtype=torch.long), penalty)
+        assert torch.equal(lg.cpu(), want)
+        r_slots, _, r_bonus, r_num = op4_ref.tree_verify(want.float(), None, tokens, children)
+        assert int(res.num_accepted) == r_num and int(res.bonus_token) == r_bonus
+        assert torch.equal(res.accepted_slots.cpu(), r_slots)
+    # with the penalty on token 10 the walk takes node 2 (token 11) instead
+    lg = logits.clone().cuda()
+    res = op4.fused_verify_commit(lg, None, tokens.cuda(), None, children, rep_penalty=1.5,
+                                  prev_tokens=prev.cuda())
+    assert res.accepted_slots[:1].tolist() == [2]

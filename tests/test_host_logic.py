@@ -32,9 +32,27 @@ def test_cpu_tensors_fail_loudly():
         m.route_and_bucket(x, router, accept, 2)
     with pytest.raises(RuntimeError, match="ROCm"):
         o.fused_verify_commit(torch.zeros(2, 8), None, torch.zeros(2), None, [[1], []])
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm"):
+        o.fused_verify_commit(torch.zeros(2, 8), torch.zeros(2, 8), torch.zeros(2), None,
+                              [[1], []], temperature=0.7)
+    with pytest.raises(ValueError, match="temperature"):
         o.fused_verify_commit(torch.zeros(2, 8), None, torch.zeros(2), None, [[1], []],
-                              temperature=0.7)
+                              temperature=-1.0)
+    with pytest.raises(ValueError, match="rep_penalty"):
+        o.fused_verify_commit(torch.zeros(2, 8), None, torch.zeros(2), None, [[1], []],
+                              rep_penalty=0.0)
+
+
+def test_tree_depth_bounds_the_sampling_commit():
+    from treemoe_spec_amd.kernels.op4_commit import _tree_depth
+
+    assert _tree_depth([[]]) == 0
+    assert _tree_depth([[1, 2], [3], [], [4], []]) == 3
+    assert _tree_depth([[1], [2], [3], []]) == 3
+    # a malformed list with a back edge still stops at N - 1
+    assert _tree_depth([[1], [0, 2], [1]]) == 2
+    # nodes unreachable from the root do not count
+    assert _tree_depth([[], [2], []]) == 0
 
 
 def test_block_m_env_is_validated(monkeypatch):

@@ -162,3 +162,119 @@ def test_kv_commit_c_equals_torch_restatement(page):
     rows = {(table[(seq_len + j) // page], (seq_len + j) % page) for j in range(len(src))}
     for p, o in changed.nonzero().tolist():
         assert (p, o) in rows
+
+
+# ---------------- sampling: inverse CDF, rep penalty, distribution ----------------
+
+def test_inverse_cdf_brute_force():
+    """Smallest j whose prefix sum exceeds u * total, by exact rational arithmetic."""
+    from fractions import Fraction
+
+    g = torch.Generator().manual_seed(11)
+    for trial in range(40):
+        v = int(torch.randint(1, 9, (1,), generator=g))
+        p = torch.rand(v, generator=g, dtype=torch.float64)
+        p[torch.rand(v, generator=g) < 0.3] = 0.0
+        if float(p.sum()) == 0.0:
+            p[v // 2] = 0.5
+        for u in torch.rand(25, generator=g, dtype=torch.float64).tolist() + [0.0]:
+            exact = [Fraction(x) for x in p.tolist()]
+            target = Fraction(u) * sum(exact)
+            run, want = Fraction(0), None
+            for j, x in enumerate(exact):
+                run += x
+                if run > target:
+                    want = j
+                    break
+            assert op4_ref.inverse_cdf(p, u) == want
+            assert p[want] > 0  # a zero-probability token is never drawn
+
+
+def test_inverse_cdf_special_cases():
+    assert op4_ref.inverse_cdf(torch.tensor([0.0, 0.0, 1.0, 0.0]), 0.999) == 2
+    assert op4_ref.inverse_cdf(torch.tensor([0.0, 0.25, 0.75]), 0.0) == 1
+    # u at the very top: the last positive entry
+    assert op4_ref.inverse_cdf(torch.tensor([0.5, 0.5, 0.0]), 1.0) == 1
+
+
+def test_inverse_cdf_distribution():
+    """Empirical frequencies of inverse_cdf(p, U) match p (6-sigma binomial)."""
+    g = torch.Generator().manual_seed(5)
+    p = torch.tensor([0.05, 0.0, 0.4, 0.15, 0.3, 0.1])
+    trials = 20000
+    u = torch.rand(trials, generator=g, dtype=torch.float64)
+    counts = np.bincount([op4_ref.inverse_cdf(p, x) for x in u.tolist()], minlength=6)
+    expect = p.double().numpy() * trials
+    sigma = np.sqrt(trials * p.double().numpy() * (1 - p.double().numpy())) + 1e-9
+    assert counts[1] == 0
+    assert np.all(np.abs(counts - expect) <= 6 * sigma)
+
+
+def test_rep_penalty_closed_form_power_of_two():
+    """penalty 2 is exact in fp32: a token listed k times is x / 2**k when
+    x > 0 and x * 2**k otherwise; unlisted and out-of-range tokens untouched."""
+    g = torch.Generator().manual_seed(2)
+    logits = torch.randn(4, 50, generator=g) * 5
+    logits[:, 7] = 0.0
+    prev = torch.tensor([3, 9, 3, 3, 7, 49, -1, 50, 9])
+    out = logits.clone()
+    op4_ref.rep_penalty_inplace(out, prev, 2.0)
+    k = np.bincount([t for t in prev.tolist() if 0 <= t < 50], minlength=50)
+    scale = torch.tensor(2.0 ** k, dtype=torch.float32)
+    expect = torch.where(logits > 0, logits / scale, logits * scale)
+    assert torch.equal(out, expect)
+    assert torch.equal(out[:, k == 0], logits[:, k == 0])
+
+
+def test_rep_penalty_order_independent():
+    g = torch.Generator().manual_seed(4)
+    logits = (torch.randn(3, 40, generator=g) * 4).to(torch.bfloat16)
+    prev = torch.randint(0, 40, (30,), generator=g)
+    a, b = logits.clone(), logits.clone()
+    op4_ref.rep_penalty_inplace(a, prev, 1.3)
+    op4_ref.rep_penalty_inplace(b, prev.flip(0), 1.3)
+    assert torch.equal(a, b)
+
+
+def test_rep_penalty_bf16_rounds_every_application():
+    """The reference stores each application to the bf16 tensor, so a token
+    listed k times rounds k times; rounding once at the end differs."""
+    g = torch.Generator().manual_seed(8)
+    logits = (torch.randn(1, 4000, generator=g) * 7).to(torch.bfloat16)
+    prev = torch.arange(4000).repeat(3)
+    stepwise = logits.clone()
+    op4_ref.rep_penalty_inplace(stepwise, prev, 1.3)
+    x = logits.float()
+    for _ in range(3):  # torch's own bf16 store after every step
+        x = torch.where(x > 0, x / 1.3, x * 1.3).to(torch.bfloat16).float()
+    assert torch.equal(stepwise.float(), x)
+    once = logits.float()
+    once = torch.where(once > 0, once / 1.3 / 1.3 / 1.3, once * 1.3 * 1.3 * 1.3)
+    assert not torch.equal(stepwise, once.to(torch.bfloat16))
+
+
+def test_tree_sampling_preserves_target_distribution():
+    """Recursive rejection sampling over a root with three children whose
+    tokens are drawn from their own draft distributions emits its first token
+    with exactly p = softmax(logits[root] / T).  A wrong residual update (no
+    clamp, no renormalisation, q of the wrong child) or a bonus drawn from p
+    instead of the residual breaks the match (6-sigma binomial bound)."""
+    v, temperature, trials = 6, 0.8, 6000
+    g = torch.Generator().manual_seed(21)
+    logits = torch.randn(4, v, generator=g) * 1.5
+    q = torch.softmax(torch.randn(4, v, generator=g) * 1.5, -1)
+    children = [[1, 2, 3], [], [], []]
+    p = torch.softmax(logits[0] / temperature, -1).double().numpy()
+    counts = np.zeros(v)
+    for _ in range(trials):
+        tokens = torch.zeros(4, dtype=torch.long)
+        for c in (1, 2, 3):
+            tokens[c] = int(torch.multinomial(q[c], 1, generator=g))
+        u = torch.rand(4, generator=g)
+        bu = float(torch.rand(1, generator=g, dtype=torch.float64))
+        _, toks, bonus, num = op4_ref.tree_verify(logits, q, tokens, children,
+                                                  temperature=temperature, uniforms=u,
+                                                  bonus_uniform=bu)
+        counts[int(toks[0]) if num else bonus] += 1
+    sigma = np.sqrt(trials * p * (1 - p))
+    assert np.all(np.abs(counts - trials * p) <= 6 * sigma)

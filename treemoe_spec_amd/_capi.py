@@ -31,6 +31,9 @@ SIGNATURES: dict[str, list] = {
     "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P, P, P, P],
     "tm_op4_kv_commit": [P, P, I64, I64, I64, I64, I64, I64, I64, P, P, P, I64, P, I64, I64,
                          I64, P],
+    "tm_op4_rep_penalty": [P, I32, I64, I64, I64, P, I64, F32, P, I64, P],
+    "tm_op4_sample_walk": [P, I32, I64, I64, I64, P, I64, P, P, P, P, P, P, F32, P, P, P, P,
+                           P],
 }
 
 TM_OBJECTIVE = {"mass": 0, "critical_path": 1}

@@ -1,6 +1,8 @@
 // op4 on gfx950: first-occurrence argmax over the vocabulary for every tree
 // node (row-chunked over many workgroups), the greedy accept walk from LDS in
 // one workgroup, and the paged KV commit of [root] + accepted path.
+#include <climits>
+
 #include "tm_common.h"
 
 namespace {
@@ -240,6 +242,257 @@ tm_kv_commit_kernel(uint8_t* __restrict__ k, uint8_t* __restrict__ v, int64_t ro
   }
 }
 
+// ------------------------------------------------------- rep penalty --
+// In place on every node row, reference `_postprocess_softmax_kernel` pass 0
+// (op4_commit.py:53-57): for each prev token t (in order),
+//   x[row, t] = x > 0 ? x / penalty : x * penalty,
+// so a token listed k times is penalised k times.  The same function is
+// applied each time, so only the count of each token matters: one workgroup
+// counts the distinct tokens in an open-addressing table (global workspace,
+// 2 * S int32 for S = table size, a power of two >= 2 * num_prev), then
+// applies each token's count to every row.  Tokens outside [0, V) are skipped.
+constexpr int kPenThreads = 1024;
+
+template <int kDtype>
+__global__ void __launch_bounds__(kPenThreads)
+tm_rep_penalty_kernel(void* __restrict__ logits, int N, int V, int64_t row_stride,
+                      const int64_t* __restrict__ prev, int num_prev, float penalty,
+                      int32_t* __restrict__ table, int S) {
+  int32_t* keys = table;
+  int32_t* counts = table + S;
+  const int tid = threadIdx.x;
+  // every table access is an agent-scope atomic, so the table is coherent at
+  // L2 whatever the L1 holds; the barriers order the three phases
+  for (int i = tid; i < S; i += kPenThreads) {
+    __hip_atomic_store(&keys[i], -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&counts[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  for (int i = tid; i < num_prev; i += kPenThreads) {
+    const int64_t t = prev[i];
+    if (t < 0 || t >= V) continue;
+    uint32_t h = ((uint32_t)t * 2654435761u) & (uint32_t)(S - 1);
+    for (int probe = 0; probe < S; ++probe) {
+      const int prior = atomicCAS(&keys[h], -1, (int)t);
+      if (prior == -1 || prior == (int)t) {
+        atomicAdd(&counts[h], 1);
+        break;
+      }
+      h = (h + 1) & (uint32_t)(S - 1);
+    }
+  }
+  __syncthreads();
+  const int64_t pairs = (int64_t)S * N;
+  for (int64_t q = tid; q < pairs; q += kPenThreads) {
+    const int slot = (int)(q % S);
+    const int row = (int)(q / S);
+    const int k = __hip_atomic_load(&counts[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k == 0) continue;
+    const int key = __hip_atomic_load(&keys[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t at = (int64_t)row * row_stride + key;
+    if (kDtype == TM_DTYPE_F32) {
+      float* x = reinterpret_cast<float*>(logits) + at;
+      float v = *x;
+      for (int r = 0; r < k; ++r) v = v > 0.0f ? v / penalty : v * penalty;
+      *x = v;
+    } else {
+      // the reference stores (rounds to bf16) after every application
+      uint16_t* x = reinterpret_cast<uint16_t*>(logits) + at;
+      uint16_t b = *x;
+      for (int r = 0; r < k; ++r) {
+        const float v = tm_bf16_to_f32(b);
+        b = tm_f32_to_bf16(v > 0.0f ? v / penalty : v * penalty);
+      }
+      *x = b;
+    }
+  }
+}
+
+// ---------------------------------------------------------- sampling --
+// Tree rejection sampling, reference `tree_verify_ref` sampling branch
+// (treemoe/ref/verify_ref.py:60-89), in one workgroup.  At the current node:
+// p = softmax(logits[node] / temperature) becomes the residual; children are
+// tried in child-list order: child c (token t) is accepted when
+// uniforms[c] < min(residual[t] / max(q_c[t], 1e-20), 1), q_c = draft_probs[c];
+// otherwise residual = max(residual - q_c, 0) / max(sum, 1e-20).  An accepted
+// child becomes the node; when every child is rejected (or at a leaf) the
+// bonus token is the inverse-CDF sample of the residual at bonus_u.  Every
+// reduction is in a fixed order, so the result is deterministic.
+constexpr int kSampThreads = 1024;
+constexpr int kSampWaves = kSampThreads / 64;
+
+struct SampShared {
+  float red[kSampWaves];
+  float bcast[2];
+  int flag;
+  int count;
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+// Workgroup sum (is_max = false) or max in a fixed order; every thread gets it.
+__device__ __forceinline__ float block_reduce(float v, bool is_max, SampShared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = is_max ? wave_max(v) : wave_sum(v);
+  if (lane == 0) sh.red[wave] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r = sh.red[0];
+    for (int w = 1; w < kSampWaves; ++w) r = is_max ? fmaxf(r, sh.red[w]) : r + sh.red[w];
+    sh.bcast[0] = r;
+  }
+  __syncthreads();
+  const float r = sh.bcast[0];
+  __syncthreads();
+  return r;
+}
+
+template <int kDtype>
+__device__ __forceinline__ float logit_at(const void* logits, int64_t at) {
+  if (kDtype == TM_DTYPE_F32) return reinterpret_cast<const float*>(logits)[at];
+  return tm_bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[at]);
+}
+
+template <int kDtype>
+__global__ void __launch_bounds__(kSampThreads)
+tm_sample_walk_kernel(const void* __restrict__ logits, int N, int V, int64_t row_stride,
+                      const float* __restrict__ q, int64_t q_stride,
+                      const int64_t* __restrict__ tokens, const int32_t* __restrict__ child_start,
+                      const int32_t* __restrict__ child_count,
+                      const int32_t* __restrict__ child_list, const float* __restrict__ uniforms,
+                      const float* __restrict__ bonus_u, float temperature,
+                      float* __restrict__ res, int64_t* __restrict__ accepted_slots,
+                      int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result) {
+  __shared__ SampShared sh;
+  const int tid = threadIdx.x;
+  int node = 0;
+  int count = 0;
+  for (;;) {
+    // residual = softmax(logits[node] / temperature)
+    const int64_t base = (int64_t)node * row_stride;
+    float m = -INFINITY;
+    for (int v = tid; v < V; v += kSampThreads)
+      m = fmaxf(m, logit_at<kDtype>(logits, base + v) / temperature);
+    m = block_reduce(m, true, sh);
+    float s = 0.0f;
+    for (int v = tid; v < V; v += kSampThreads)
+      s = s + tm_expf_det(logit_at<kDtype>(logits, base + v) / temperature - m);
+    s = block_reduce(s, false, sh);
+    for (int v = tid; v < V; v += kSampThreads)
+      res[v] = tm_expf_det(logit_at<kDtype>(logits, base + v) / temperature - m) / s;
+    __syncthreads();
+
+    const int st = child_start[node];
+    const int cnt = child_count[node];
+    int taken = -1;
+    for (int j = 0; j < cnt; ++j) {
+      const int c = child_list[st + j];
+      if (tid == 0) {
+        const int64_t tok = tokens[c];
+        int ok = 0;
+        if (tok >= 0 && tok < V) {
+          float ratio = res[tok] / fmaxf(q[(int64_t)c * q_stride + tok], 1e-20f);
+          ratio = fminf(ratio, 1.0f);
+          ok = uniforms[c] < ratio ? 1 : 0;
+        }
+        sh.flag = ok;
+      }
+      __syncthreads();
+      const int ok = sh.flag;
+      __syncthreads();
+      if (ok) {
+        taken = c;
+        break;
+      }
+      const float* qc = q + (int64_t)c * q_stride;
+      float part = 0.0f;
+      for (int v = tid; v < V; v += kSampThreads) {
+        const float r = fmaxf(res[v] - qc[v], 0.0f);
+        res[v] = r;
+        part = part + r;
+      }
+      const float tot = fmaxf(block_reduce(part, false, sh), 1e-20f);
+      for (int v = tid; v < V; v += kSampThreads) res[v] = res[v] / tot;
+      __syncthreads();
+    }
+    if (taken >= 0 && count < N) {
+      if (tid == 0) {
+        accepted_slots[count] = taken;
+        accepted_tokens[count] = tokens[taken];
+      }
+      ++count;
+      node = taken;
+      continue;
+    }
+    break;
+  }
+
+  // bonus: smallest j with res[0] + .. + res[j] > bonus_u * total, chunked
+  // prefix sums (thread t owns a contiguous chunk; chunk sums scanned in
+  // thread order)
+  const int cs = (V + kSampThreads - 1) / kSampThreads;
+  const int lo = min(V, tid * cs), hi = min(V, lo + cs);
+  float csum = 0.0f;
+  for (int v = lo; v < hi; ++v) csum = csum + res[v];
+  // exclusive scan of chunk sums over the workgroup, in thread order
+  __shared__ float s_chunk[kSampThreads];
+  s_chunk[tid] = csum;
+  __syncthreads();
+  if (tid == 0) {
+    float run = 0.0f;
+    for (int t = 0; t < kSampThreads; ++t) {
+      const float c = s_chunk[t];
+      s_chunk[t] = run;
+      run = run + c;
+    }
+    sh.bcast[1] = run;
+    sh.flag = INT_MAX;
+  }
+  __syncthreads();
+  const float target = bonus_u[0] * sh.bcast[1];
+  float run = s_chunk[tid];
+  // exactly one chunk satisfies this (the boundaries are the same rounded sums)
+  if (run <= target && target < run + csum) {
+    int pick = hi - 1;
+    for (int v = lo; v < hi; ++v) {
+      run = run + res[v];
+      if (run > target) {
+        pick = v;
+        break;
+      }
+    }
+    atomicMin(&sh.flag, pick);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int bonus = sh.flag;
+    if (bonus == INT_MAX) {  // target at or past the total: last nonzero entry
+      bonus = 0;
+      for (int v = V - 1; v >= 0; --v)
+        if (res[v] > 0.0f) { bonus = v; break; }
+    }
+    result[0] = bonus;
+    result[1] = count;
+    result[2] = node;
+    sh.count = count;
+  }
+  __syncthreads();
+  for (int i = sh.count + tid; i < N; i += kSampThreads) {
+    accepted_slots[i] = -1;
+    accepted_tokens[i] = -1;
+  }
+}
+
 }  // namespace
 
 extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
@@ -280,6 +533,57 @@ extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int6
   hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, (hipStream_t)stream,
                      partial, (int)parts, (int)N, tokens, child_start, child_count, child_list,
                      (int)max_depth, argmax, accepted_slots, accepted_tokens, result);
+  TM_HIP_CHECK_LAUNCH();
+  return TM_OK;
+}
+
+extern "C" int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V,
+                                  int64_t row_stride, const int64_t* prev_tokens,
+                                  int64_t num_prev, float penalty, int32_t* table,
+                                  int64_t table_size, void* stream) {
+  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || num_prev < 1 ||
+      num_prev > (1 << 24))
+    return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
+  if (table_size < 2 * num_prev || (table_size & (table_size - 1)) != 0 || table_size > (1 << 26))
+    return TM_ERR_SHAPE;
+  if (!(penalty > 0.0f)) return TM_ERR_ARG;
+  if (dtype == TM_DTYPE_F32) {
+    hipLaunchKernelGGL(tm_rep_penalty_kernel<TM_DTYPE_F32>, dim3(1), dim3(kPenThreads), 0,
+                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, prev_tokens,
+                       (int)num_prev, penalty, table, (int)table_size);
+  } else {
+    hipLaunchKernelGGL(tm_rep_penalty_kernel<TM_DTYPE_BF16>, dim3(1), dim3(kPenThreads), 0,
+                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, prev_tokens,
+                       (int)num_prev, penalty, table, (int)table_size);
+  }
+  TM_HIP_CHECK_LAUNCH();
+  return TM_OK;
+}
+
+extern "C" int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int64_t V,
+                                  int64_t row_stride, const float* draft_probs, int64_t q_stride,
+                                  const int64_t* tokens, const int32_t* child_start,
+                                  const int32_t* child_count, const int32_t* child_list,
+                                  const float* uniforms, const float* bonus_u,
+                                  float temperature, float* residual,
+                                  int64_t* accepted_slots, int64_t* accepted_tokens,
+                                  int64_t* result, void* stream) {
+  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || q_stride < V)
+    return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
+  if (!(temperature > 0.0f)) return TM_ERR_ARG;
+  if (dtype == TM_DTYPE_F32) {
+    hipLaunchKernelGGL(tm_sample_walk_kernel<TM_DTYPE_F32>, dim3(1), dim3(kSampThreads), 0,
+                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, draft_probs,
+                       q_stride, tokens, child_start, child_count, child_list, uniforms, bonus_u,
+                       temperature, residual, accepted_slots, accepted_tokens, result);
+  } else {
+    hipLaunchKernelGGL(tm_sample_walk_kernel<TM_DTYPE_BF16>, dim3(1), dim3(kSampThreads), 0,
+                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, draft_probs,
+                       q_stride, tokens, child_start, child_count, child_list, uniforms, bonus_u,
+                       temperature, residual, accepted_slots, accepted_tokens, result);
+  }
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }

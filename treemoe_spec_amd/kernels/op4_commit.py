@@ -11,8 +11,21 @@ Same call signature as the reference ``fused_verify_commit``
                        tree scratch pages to positions seq_len, seq_len+1, ...
 
 ``kv.seq_len`` advances by num_accepted + 1, which reads num_accepted back to
-the host exactly like the reference (:267).  Sampling mode (temperature > 0)
-and the repetition penalty are not implemented and raise.
+the host exactly like the reference (:267).
+
+Greedy with rep_penalty != 1 (reference :201-214) first penalises the logits
+in place (``tm_op4_rep_penalty``; without prev_tokens token 0 is penalised, as
+in the reference), then takes the argmax of the penalised logits.  The
+reference takes it over their rounded softmax, which can differ only where
+rounding makes two probabilities equal.
+
+Sampling (temperature > 0) follows the reference's routing of that mode to
+``tree_verify_ref`` (:187-196): the walk is unbounded (max_depth and
+rep_penalty are not used), the accept draws are ``torch.rand(N, generator)``
+on the logits' device as in the reference, and the bonus token is an
+inverse-CDF draw of the residual at one more uniform from the same generator
+(the reference calls torch.multinomial: same distribution, different use of
+the random stream).  One launch, ``tm_op4_sample_walk``.
 """
 
 from __future__ import annotations
@@ -41,6 +54,28 @@ def argmax_workspace(n: int, device) -> torch.Tensor:
     return torch.empty(n * _capi.TM_OP4_MAX_PARTS * 8, dtype=torch.uint8, device=device)
 
 
+def _penalty_table_size(num_prev: int) -> int:
+    return 1 << max(4, (2 * num_prev - 1).bit_length())
+
+
+def _apply_rep_penalty(logits: torch.Tensor, dtype: int, prev_tokens, rep_penalty: float,
+                       stream: int) -> None:
+    n, v = logits.shape
+    dev = logits.device
+    if prev_tokens is None:
+        prev = torch.zeros(1, dtype=torch.int64, device=dev)  # reference :209
+    else:
+        prev = prev_tokens.to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
+        if prev.numel() == 0:
+            return
+        # tokens outside [0, vocab) are skipped by the kernel (the reference
+        # would index past the row)
+    size = _penalty_table_size(prev.numel())
+    table = torch.empty(2 * size, dtype=torch.int32, device=dev)
+    call("tm_op4_rep_penalty", ptr(logits), dtype, n, v, logits.stride(0), ptr(prev),
+         prev.numel(), float(rep_penalty), ptr(table), size, stream)
+
+
 def _children_csr(children: list[list[int]], n: int, device) -> torch.Tensor:
     """[starts | counts | flat] int32 in one host->device copy."""
     if len(children) != n:
@@ -56,6 +91,21 @@ def _children_csr(children: list[list[int]], n: int, device) -> torch.Tensor:
     return torch.from_numpy(packed.astype(np.int32)).to(device, non_blocking=False)
 
 
+def _tree_depth(children: list[list[int]]) -> int:
+    """Longest root-to-node path (edges) reachable from node 0, at most N - 1;
+    bounds the sampling walk, which the reference leaves unbounded."""
+    n = len(children)
+    depth, frontier, seen = 0, [0], {0}
+    while depth < n - 1:
+        nxt = [c for node in frontier for c in children[node] if c not in seen]
+        if not nxt:
+            break
+        seen.update(nxt)
+        frontier = nxt
+        depth += 1
+    return depth
+
+
 def fused_verify_commit(
     target_logits: torch.Tensor,     # [N, V] fp32 or bf16
     draft_probs: torch.Tensor,       # [N, V] (unused by greedy verification)
@@ -69,10 +119,10 @@ def fused_verify_commit(
     max_depth: int = 6,
     generator: torch.Generator | None = None,
 ) -> VerifyResult:
-    if temperature != 0.0 or rep_penalty != 1.0:
-        raise NotImplementedError(
-            "treemoe_spec_amd implements greedy verification (temperature == 0, "
-            "rep_penalty == 1) only")
+    if temperature < 0.0:
+        raise ValueError("temperature must be >= 0")
+    if rep_penalty <= 0.0:
+        raise ValueError("rep_penalty must be > 0")
     if not target_logits.is_cuda:
         raise RuntimeError("treemoe_spec_amd op4 runs on ROCm devices only; got a CPU tensor")
     if target_logits.dim() != 2 or target_logits.stride(1) != 1:
@@ -89,20 +139,38 @@ def fused_verify_commit(
     if tokens.numel() != n:
         raise ValueError("tree_tokens must have one entry per node")
     csr = _children_csr(children, n, dev)
-    argmax = torch.empty(n, dtype=torch.int32, device=dev)
     slots = torch.empty(n, dtype=torch.int64, device=dev)
     toks = torch.empty(n, dtype=torch.int64, device=dev)
     result = torch.empty(3, dtype=torch.int64, device=dev)
     stream = _capi.stream_of(dev)
-    call("tm_op4_argmax_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
-         ptr(tokens), ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n, max_depth, ptr(argmax),
-         ptr(slots), ptr(toks), ptr(result), ptr(argmax_workspace(n, dev)), stream)
+    if temperature != 0.0:
+        q = draft_probs
+        if (q is None or not q.is_cuda or q.dtype != torch.float32 or q.dim() != 2
+                or tuple(q.shape) != (n, v) or q.stride(1) != 1):
+            raise ValueError("sampling needs draft_probs [N, V] float32 on the logits' device "
+                             "with unit stride along V")
+        uniforms = torch.rand(n, generator=generator, device=dev)  # reference verify_ref.py:51
+        bonus_u = torch.rand(1, generator=generator, device=dev)
+        residual = torch.empty(v, dtype=torch.float32, device=dev)
+        call("tm_op4_sample_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
+             ptr(q), q.stride(0), ptr(tokens), ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n,
+             ptr(uniforms), ptr(bonus_u), float(temperature), ptr(residual), ptr(slots),
+             ptr(toks), ptr(result), stream)
+        commit_depth = _tree_depth(children)
+    else:
+        if rep_penalty != 1.0:
+            _apply_rep_penalty(target_logits, dtype, prev_tokens, rep_penalty, stream)
+        argmax = torch.empty(n, dtype=torch.int32, device=dev)
+        call("tm_op4_argmax_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
+             ptr(tokens), ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n, max_depth, ptr(argmax),
+             ptr(slots), ptr(toks), ptr(result), ptr(argmax_workspace(n, dev)), stream)
+        commit_depth = max_depth
     res = VerifyResult(accepted_slots=slots, accepted_tokens=toks,
                        bonus_token=result[0], num_accepted=result[1])
     if kv is not None:
         # commit [root] + accepted path: the root token's KV (tree slot 0) is
         # part of the committed sequence too (reference :242-247).
-        m_max = max_depth + 1
+        m_max = commit_depth + 1
         kv._ensure_capacity(kv.seq_len + m_max)
         table, scratch = kv.device_tables(dev)
         k = kv.k
@@ -113,6 +181,6 @@ def fused_verify_commit(
         call("tm_op4_kv_commit", ptr(k), ptr(kv.v), k.element_size(), k.shape[0],
              k.shape[3] * k.shape[4], k.stride(0), k.stride(1), k.stride(2), kv.block_size,
              ptr(slots), ptr(result), ptr(scratch), len(kv.tree_pages), ptr(table),
-             len(kv.block_table), kv.seq_len, max_depth, stream)
+             len(kv.block_table), kv.seq_len, commit_depth, stream)
         kv.seq_len += int(res.num_accepted) + 1
     return res
