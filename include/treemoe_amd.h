@@ -6,6 +6,7 @@
  *
  *   op1  tree_moe_forward / route_experts   treemoe/kernels/op1_tree_moe.py:641-802
  *   op4  fused_verify_commit                treemoe/kernels/op4_commit.py:170-272
+ *   tree attention (verification forward)   treemoe/model/mixtral.py:208-250
  *
  * Conventions (all entry points):
  *   - plain device pointers and sizes; no torch types, no allocation inside;
@@ -268,6 +269,57 @@ int tm_op4_kv_commit(void* k, void* v, int64_t elem_bytes, int64_t L,
                      int64_t num_scratch_pages, const int32_t* block_table,
                      int64_t num_table_pages, int64_t seq_len,
                      int64_t max_depth, void* stream);
+
+/*
+ * Tree attention: the verification forward's attention over the paged KV
+ * cache.  Replaces, for the tree branch of `MixtralForward._attention`
+ * (treemoe/model/mixtral.py:208-250): `PagedKVCache.write_tree`
+ * (treemoe/model/kv_cache.py:80-86), `gather_with_tail` (:125-145), the mask
+ * (mixtral.py:211-218) and `F.scaled_dot_product_attention(..., enable_gqa=True)`.
+ *
+ * Node i, query head h (kv head h / (Hq / kvh)) attends to every prefix
+ * position 0 .. seq_len-1 and to tree node j when bit j of mask row i is set:
+ *   out[i, h] = softmax_j(scale * q[i, h] . k_j) v_j,
+ * prefix k_j/v_j read in place from the layer's cache pages: page
+ * block_table[pos / page_size], slot pos % page_size; tree k_j/v_j read from
+ * k_tail/v_tail [N, kvh, hd].  With write_tree the tree rows are also stored
+ * in the scratch pages (node j: page scratch_pages[j / page_size], slot
+ * j % page_size), as write_tree does.  A row with no visible key gives 0.
+ *
+ * q, out: [N, Hq, hd] bf16 (node strides q_stride, out_stride; heads
+ * contiguous).  k_cache, v_cache: this layer's [pages, page_size, kvh, hd]
+ * bf16 with strides stride_page, stride_slot (elements).  mask_bits: [N,
+ * ceil(N/64)] u64 (tm_tree_mask_pack).  hd = 128, N <= 256, page_size a power
+ * of two; 16-byte aligned pointers and strides.  chunk_keys: keys per
+ * workgroup (0 = automatic); workspace: tm_tree_attention_plan's size.
+ */
+int tm_tree_attention(const void* q, int64_t q_stride, const void* k_tail,
+                      const void* v_tail, int64_t tail_stride, void* k_cache,
+                      void* v_cache, int64_t stride_page, int64_t stride_slot,
+                      int64_t page_size, const int32_t* block_table,
+                      int64_t num_table_pages, int64_t seq_len,
+                      const int32_t* scratch_pages, int64_t num_scratch_pages,
+                      int write_tree, const uint64_t* mask_bits, int64_t N,
+                      int64_t Hq, int64_t kvh, int64_t hd, float scale, void* out,
+                      int64_t out_stride, int64_t chunk_keys, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/*
+ * Key chunking of tm_tree_attention for these sizes: the number of key chunks
+ * and the workspace bytes it needs (0 when one chunk covers every key).  Host
+ * only; no counterpart in the reference, which has no workspace.
+ */
+int tm_tree_attention_plan(int64_t N, int64_t Hq, int64_t kvh, int64_t hd,
+                           int64_t seq_len, int64_t page_size, int64_t chunk_keys,
+                           int64_t* chunks, int64_t* workspace_bytes);
+
+/*
+ * Bit-pack the tree's [N, N] bool ancestor mask (engine/tree.py:164-171
+ * builds it; row stride in bytes) into [N, ceil(N/64)] u64 words, bit j of
+ * word w of row i = mask[i][64 w + j].
+ */
+int tm_tree_mask_pack(const uint8_t* mask, int64_t N, int64_t row_stride,
+                      uint64_t* bits, void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,7 +24,8 @@ def test_header_declares_entry_points():
     for n in ("tm_version", "tm_status_string", "tm_op1_router_gates", "tm_op1_route_bucket",
               "tm_op1_gemm1", "tm_op1_gemm2", "tm_op1_combine", "tm_op1_prefill_gemm1",
               "tm_op1_prefill_gemm2", "tm_op4_argmax_walk", "tm_op4_rep_penalty",
-              "tm_op4_sample_walk", "tm_op4_kv_commit"):
+              "tm_op4_sample_walk", "tm_op4_kv_commit", "tm_tree_attention",
+              "tm_tree_attention_plan", "tm_tree_mask_pack"):
         assert n in names
 
 
@@ -45,6 +46,57 @@ def test_status_strings():
     assert lib.tm_status_string(0) == b"ok"
     for code in (1001, 1002, 1003):
         assert lib.tm_status_string(code) not in (b"ok", b"unknown status")
+
+
+def _attn_args(**kw):
+    """tm_tree_attention arguments at the config-4 shape (null pointers)."""
+    a = dict(q=0, q_stride=4096, k_tail=0, v_tail=0, tail_stride=1024, k_cache=0, v_cache=0,
+             stride_page=16 * 1024, stride_slot=1024, page_size=16, block_table=0,
+             num_table_pages=256, seq_len=4096, scratch_pages=0, num_scratch_pages=4,
+             write_tree=1, mask_bits=0, N=64, Hq=32, kvh=8, hd=128, scale=0.088, out=0,
+             out_stride=4096, chunk_keys=0, workspace=0, workspace_bytes=0, stream=0)
+    a.update(kw)
+    return ("tm_tree_attention", *a.values())
+
+
+@pytest.mark.parametrize("call,expect", [
+    (_attn_args(), 1001),                                  # workspace too small
+    (_attn_args(hd=64, workspace_bytes=1 << 30), 1001),
+    (_attn_args(N=0, workspace_bytes=1 << 30), 1001),
+    (_attn_args(N=257, workspace_bytes=1 << 30), 1001),
+    (_attn_args(page_size=24, workspace_bytes=1 << 30), 1001),
+    (_attn_args(Hq=12, workspace_bytes=1 << 30), 1001),    # Hq % kvh
+    (_attn_args(num_table_pages=255, workspace_bytes=1 << 30), 1001),
+    (_attn_args(num_scratch_pages=3, workspace_bytes=1 << 30), 1001),
+    (_attn_args(q=8, workspace_bytes=1 << 30), 1002),
+    (_attn_args(stride_slot=1028, stride_page=16 * 1028, workspace_bytes=1 << 30), 1002),
+    (_attn_args(scale=0.0, workspace_bytes=1 << 30), 1003),
+    (_attn_args(chunk_keys=-1, workspace_bytes=1 << 30), 1003),
+    (("tm_tree_mask_pack", 0, 0, 1, 0, 0), 1001),
+    (("tm_tree_mask_pack", 0, 4, 4, 4, 0), 1002),
+])
+def test_tree_attention_argument_errors(call, expect):
+    from treemoe_spec_amd import _capi
+
+    name, *args = call
+    assert getattr(_capi.lib(), name)(*args) == expect
+
+
+def test_tree_attention_plan():
+    import ctypes
+
+    from treemoe_spec_amd import _capi
+
+    chunks, ws = ctypes.c_int64(), ctypes.c_int64()
+    plan = _capi.lib().tm_tree_attention_plan
+    assert plan(64, 32, 8, 128, 0, 16, 0, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    assert chunks.value == 1 and ws.value == 0
+    assert plan(64, 32, 8, 128, 4096, 16, 64, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    # 65 chunks x 8 heads x 4 row blocks x 4 waves x (64 lanes x 32 + 128) floats
+    assert chunks.value == 65 and ws.value == 65 * 8 * 4 * 4 * (64 * 32 + 128) * 4
+    assert plan(64, 32, 8, 128, 4096, 16, 0, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    assert 8 * 4 * chunks.value >= 256   # automatic chunks fill the 256 CUs
+    assert plan(64, 32, 8, 64, 4096, 16, 0, ctypes.byref(chunks), ctypes.byref(ws)) == 1001
 
 
 @pytest.mark.parametrize("call,expect", [

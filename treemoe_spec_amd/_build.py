@@ -22,7 +22,8 @@ OBJ_DIR = PKG / "_build"
 ORACLE_C = ROOT / "oracle" / "c"
 ORACLE_LIB = ROOT / "oracle" / "liboracle_c.so"
 
-HIP_SOURCES = ["capi.hip", "op1_route.hip", "op1_gemm.hip", "op1_prefill.hip", "op4_verify.hip"]
+HIP_SOURCES = ["capi.hip", "op1_route.hip", "op1_gemm.hip", "op1_prefill.hip", "op4_verify.hip",
+               "tree_attn.hip"]
 ARCH = os.environ.get("TREEMOE_AMD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -34,6 +34,10 @@ SIGNATURES: dict[str, list] = {
     "tm_op4_rep_penalty": [P, I32, I64, I64, I64, P, I64, F32, P, I64, P],
     "tm_op4_sample_walk": [P, I32, I64, I64, I64, P, I64, P, P, P, P, P, P, F32, P, P, P, P,
                            P],
+    "tm_tree_attention": [P, I64, P, P, I64, P, P, I64, I64, I64, P, I64, I64, P, I64, I32, P,
+                          I64, I64, I64, I64, F32, P, I64, I64, P, I64, P],
+    "tm_tree_attention_plan": [I64, I64, I64, I64, I64, I64, I64, P, P],
+    "tm_tree_mask_pack": [P, I64, I64, P, P],
 }
 
 TM_OBJECTIVE = {"mass": 0, "critical_path": 1}

@@ -1,0 +1,518 @@
+// Tree attention on gfx950: every node of a draft tree attends to the whole
+// committed prefix and to its own ancestors (and itself) in the tree.
+//
+// Keys 0 .. seq_len-1 are the prefix, read in place from the paged cache
+// through the block table (no gather copy); keys seq_len .. seq_len+N-1 are
+// the tree's own K/V rows.  Query head h reads KV head h / group.
+//
+// Work decomposition.  For one KV head the group * N query rows (rows ordered
+// head-in-group major, node minor) share every K/V byte, so a workgroup takes
+// 64 of those rows (4 waves x 16) against one chunk of keys; the K/V of the
+// chunk is staged through LDS 64 keys at a time and each key byte is read from
+// HBM once per (KV head, chunk), by the row blocks of that pair, which are
+// launched on one XCD (launch indices congruent mod 8) so they share its L2.
+//
+// Per wave and 64-key stage (v_mfma_f32_16x16x32_bf16 throughout):
+//   S^T = K Q^T    A = K rows from LDS, B = Q^T held in registers,
+//                  lane l gets S^T[key 16t + 4(l/16) + i][query l%16];
+//   online softmax in base 2, per query (= per lane column), the 4 lanes of a
+//                  query combined by two xor shuffles;
+//   O^T += V^T P^T B = P^T straight from the S^T registers: the MFMA's k slots
+//                  8(l/16) + j are mapped to keys 32s + 4(l/16) + j (j < 4) and
+//                  32s + 16 + 4(l/16) + j - 4, which are exactly the keys the
+//                  lane holds; A = V^T read with the same key map from a
+//                  transposed copy of V in LDS.
+// A chunk's unnormalised O^T, running max and sum go to a workspace and a
+// second kernel combines the chunks in chunk order (deterministic); with one
+// chunk the first kernel writes the normalised output itself.
+#include <algorithm>
+#include <cmath>
+
+#include "tm_common.h"
+
+namespace {
+
+constexpr int kHD = 128;                    // head dim
+constexpr int kThreads = 256;               // 4 waves
+constexpr int kRows = 64;                   // query rows per workgroup
+constexpr int kKeys = 64;                   // keys per LDS stage
+constexpr int kKStride = kHD * 2 + 16;      // bytes per K row in LDS (272)
+constexpr int kVStride = kKeys * 2 + 8;     // bytes per V^T row in LDS (136)
+constexpr int kKBytes = kKeys * kKStride;   // 17,408
+constexpr int kVBytes = kHD * kVStride;     // 17,408
+constexpr int kStage = kKBytes + kVBytes;   // 34,816
+constexpr int kMaxPages = 512;              // block-table entries staged per chunk
+constexpr int kMaxNodes = 256;              // tree nodes (mask words per row <= 4)
+constexpr int kTargetGroups = 512;          // workgroups the planner aims for
+constexpr int kMinChunk = 256;              // keys per chunk, lower bound
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+struct AttnParams {
+  const uint16_t* q;          // [N, Hq, HD], node stride q_stride (elements)
+  const uint16_t* k_tail;     // [N, kvh, HD], node stride tail_stride
+  const uint16_t* v_tail;
+  uint16_t* k_cache;          // this layer's [pages, page, kvh, HD]
+  uint16_t* v_cache;
+  const int32_t* block_table;
+  const int32_t* scratch_pages;
+  const uint64_t* mask_bits;  // [N, mask_words], bit j of row i: node j visible
+  uint16_t* out;              // [N, Hq, HD], node stride out_stride
+  float* part;                // chunk partials (chunks > 1)
+  float* stats;
+  int64_t q_stride, tail_stride, out_stride, stride_page, stride_slot;
+  int page_shift, seq_len, n, hq, kvh, group, rows, row_blocks, chunks, chunk_len, pairs;
+  int mask_words, write_tree;
+  float scale_log2;
+};
+
+__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return (uint32_t)tm_f32_to_bf16(lo) | ((uint32_t)tm_f32_to_bf16(hi) << 16);
+}
+
+// Stage layout: thread t stages keys 4 * quad + r (r = 0..3) at head-dim
+// elements 8 * part .. +7, with quad = (t & 3) + 4 * (t >> 6) and
+// part = (t >> 2) & 15; this order keeps both the K row writes and the
+// transposed V writes free of LDS bank conflicts.
+struct Stage {
+  u32x4_t k[4];
+  u32x4_t v[4];
+};
+
+__device__ __forceinline__ void load_stage(const AttnParams& p, const int* s_pages, int kb,
+                                           int c0, int c1, int kvhead, int quad, int part,
+                                           Stage& st) {
+  const int64_t head_off = (int64_t)kvhead * kHD + part * 8;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int key = kb + 4 * quad + r;
+    const bool valid = key < c1;
+    int64_t off;
+    const uint16_t* kb_ptr;
+    const uint16_t* vb_ptr;
+    if (valid && key < p.seq_len) {
+      // key < min(c1, seq_len): its page is among the chunk's staged entries
+      const int page = s_pages[(key >> p.page_shift) - (c0 >> p.page_shift)];
+      off = (int64_t)page * p.stride_page +
+            (int64_t)(key & ((1 << p.page_shift) - 1)) * p.stride_slot + head_off;
+      kb_ptr = p.k_cache;
+      vb_ptr = p.v_cache;
+    } else {
+      const int node = valid ? key - p.seq_len : 0;  // row 0 stands in past the end
+      off = (int64_t)node * p.tail_stride + head_off;
+      kb_ptr = p.k_tail;
+      vb_ptr = p.v_tail;
+    }
+    const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(kb_ptr + off);
+    const u32x4_t vv = *reinterpret_cast<const u32x4_t*>(vb_ptr + off);
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+    st.k[r] = valid ? kv : zero;
+    st.v[r] = valid ? vv : zero;
+  }
+}
+
+__device__ __forceinline__ void store_stage(uint8_t* buf, int quad, int part, const Stage& st) {
+  uint8_t* kl = buf;
+  uint8_t* vl = buf + kKBytes;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    *reinterpret_cast<u32x4_t*>(kl + (4 * quad + r) * kKStride + part * 16) = st.k[r];
+  // V^T[hd][key]: for head-dim element 8 * part + j, the 4 keys of this quad
+  // side by side (8 bytes)
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int w = j >> 1;
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    u32x2_t pk;
+    pk.x = __builtin_amdgcn_perm(st.v[1][w], st.v[0][w], sel);
+    pk.y = __builtin_amdgcn_perm(st.v[3][w], st.v[2][w], sel);
+    *reinterpret_cast<u32x2_t*>(vl + (8 * part + j) * kVStride + quad * 8) = pk;
+  }
+}
+
+__global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_buf[2 * kStage];
+  __shared__ int s_pages[kMaxPages];
+
+  const int x8 = blockIdx.x & 7, y = blockIdx.x >> 3;
+  const int rb = y % p.row_blocks;
+  const int pair = (y / p.row_blocks) * 8 + x8;
+  if (pair >= p.pairs) return;
+  const int kvhead = pair / p.chunks;
+  const int chunk = pair % p.chunks;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int s_total = p.seq_len + p.n;
+  const int c0 = chunk * p.chunk_len;
+  const int c1 = min(c0 + p.chunk_len, s_total);
+  const int quad = (tid & 3) + 4 * (tid >> 6);
+  const int part = (tid >> 2) & 15;
+
+  // tree rows of this KV head into the scratch pages (one workgroup per head)
+  if (p.write_tree && rb == 0 && chunk == p.chunks - 1) {
+    for (int u = tid; u < p.n * 16; u += kThreads) {
+      const int node = u >> 4, pc = u & 15;
+      const int64_t src = (int64_t)node * p.tail_stride + kvhead * kHD + pc * 8;
+      const int64_t dst = (int64_t)p.scratch_pages[node >> p.page_shift] * p.stride_page +
+                          (int64_t)(node & ((1 << p.page_shift) - 1)) * p.stride_slot +
+                          kvhead * kHD + pc * 8;
+      *reinterpret_cast<u32x4_t*>(p.k_cache + dst) =
+          *reinterpret_cast<const u32x4_t*>(p.k_tail + src);
+      *reinterpret_cast<u32x4_t*>(p.v_cache + dst) =
+          *reinterpret_cast<const u32x4_t*>(p.v_tail + src);
+    }
+  }
+
+  // block-table entries of the chunk's prefix keys
+  const int pre_end = min(c1, p.seq_len);
+  const int npages = pre_end > c0 ? ((pre_end - 1) >> p.page_shift) - (c0 >> p.page_shift) + 1 : 0;
+  for (int i = tid; i < npages; i += kThreads)
+    s_pages[i] = p.block_table[(c0 >> p.page_shift) + i];
+
+  // this lane's query row: Q^T fragments and the tree-mask row
+  const int row = rb * kRows + wave * 16 + c16;
+  const bool row_ok = row < p.rows;
+  const int node = row_ok ? row % p.n : 0;
+  const int head = kvhead * p.group + (row_ok ? row / p.n : 0);
+  u32x4_t qf[kHD / 32];
+  {
+    const uint16_t* qrow = p.q + (int64_t)node * p.q_stride + (int64_t)head * kHD + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < kHD / 32; ++ks) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + 32 * ks);
+      const u32x4_t zero = {0u, 0u, 0u, 0u};
+      qf[ks] = row_ok ? v : zero;
+    }
+  }
+  uint64_t mw[4] = {0, 0, 0, 0};
+  if (c1 > p.seq_len) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w)
+      if (w < p.mask_words) mw[w] = p.mask_bits[(int64_t)node * p.mask_words + w];
+  }
+  __syncthreads();  // s_pages
+
+  Stage st;
+  load_stage(p, s_pages, c0, c0, c1, kvhead, quad, part, st);
+  store_stage(s_buf, quad, part, st);
+  __syncthreads();
+
+  f32x4_t acc[kHD / 16];
+#pragma unroll
+  for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+
+  const int nstage = (c1 - c0 + kKeys - 1) / kKeys;
+  for (int s = 0; s < nstage; ++s) {
+    const int kb = c0 + s * kKeys;
+    // next stage's loads go out before this stage's MFMAs (the last stage
+    // reloads itself: unconditional, so the wait counts stay exact)
+    const int kn = c0 + min(s + 1, nstage - 1) * kKeys;
+    load_stage(p, s_pages, kn, c0, c1, kvhead, quad, part, st);
+
+    const uint8_t* kl = s_buf + (s & 1) * kStage;
+    const uint8_t* vl = kl + kKBytes;
+    // S^T tiles: keys 16t .. 16t+15 of the stage
+    f32x4_t sc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < kHD / 32; ++ks) {
+        const u32x4_t a =
+            *reinterpret_cast<const u32x4_t*>(kl + (16 * t + c16) * kKStride + ks * 64 + g * 16);
+        sc[t] = mfma16(a, qf[ks], sc[t]);
+      }
+    }
+    // scale, mask, running max
+    const bool all_visible = kb + kKeys <= min(c1, p.seq_len);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = sc[t][i] * p.scale_log2;
+        if (!all_visible) {
+          const int key = kb + 16 * t + 4 * g + i;
+          bool vis = key < c1;
+          if (key >= p.seq_len) {
+            const int j = key - p.seq_len;
+            const uint64_t word = j < 64 ? mw[0] : j < 128 ? mw[1] : j < 192 ? mw[2] : mw[3];
+            vis = vis && ((word >> (j & 63)) & 1u);
+          }
+          v = vis ? v : -INFINITY;
+        }
+        sc[t][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float base = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = exp2f(m_run - base);
+    m_run = m_new;
+    float lsum = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = exp2f(sc[t][i] - base);
+        sc[t][i] = e;
+        lsum += e;
+      }
+    }
+    l_run = l_run * alpha + lsum;
+#pragma unroll
+    for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] *= alpha;
+    // O^T += V^T P^T over two 32-key k-steps
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      u32x4_t b;
+      b.x = pack_bf16(sc[2 * k2][0], sc[2 * k2][1]);
+      b.y = pack_bf16(sc[2 * k2][2], sc[2 * k2][3]);
+      b.z = pack_bf16(sc[2 * k2 + 1][0], sc[2 * k2 + 1][1]);
+      b.w = pack_bf16(sc[2 * k2 + 1][2], sc[2 * k2 + 1][3]);
+#pragma unroll
+      for (int tt = 0; tt < kHD / 16; ++tt) {
+        const uint8_t* vr = vl + (16 * tt + c16) * kVStride + (32 * k2 + 4 * g) * 2;
+        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
+        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 32);
+        const u32x4_t a = {lo.x, lo.y, hi.x, hi.y};
+        acc[tt] = mfma16(a, b, acc[tt]);
+      }
+    }
+    store_stage(s_buf + ((s + 1) & 1) * kStage, quad, part, st);
+    __syncthreads();
+  }
+
+  // the 4 lanes of a query hold partial sums over disjoint keys
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+
+  if (p.chunks == 1) {
+    if (row_ok) {
+      const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+      uint16_t* orow = p.out + (int64_t)node * p.out_stride + (int64_t)head * kHD + 4 * g;
+#pragma unroll
+      for (int tt = 0; tt < kHD / 16; ++tt) {
+        u32x2_t o;
+        o.x = pack_bf16(acc[tt][0] * inv, acc[tt][1] * inv);
+        o.y = pack_bf16(acc[tt][2] * inv, acc[tt][3] * inv);
+        *reinterpret_cast<u32x2_t*>(orow + 16 * tt) = o;
+      }
+    }
+    return;
+  }
+  const int64_t slot = ((int64_t)(kvhead * p.row_blocks + rb) * p.chunks + chunk) * 4 + wave;
+  float* pp = p.part + slot * (kHD / 16) * 256 + lane * 4;
+#pragma unroll
+  for (int tt = 0; tt < kHD / 16; ++tt) *reinterpret_cast<f32x4_t*>(pp + tt * 256) = acc[tt];
+  float* sp = p.stats + slot * 128 + lane * 2;
+  sp[0] = m_run;
+  sp[1] = l_run;
+}
+
+// One workgroup per (KV head, row block): O = sum_c w_c O_c / sum_c w_c l_c
+// with w_c = 2^(m_c - max m), chunks in order.
+__global__ void __launch_bounds__(kThreads) tm_tree_attn_combine_kernel(AttnParams p) {
+  const int kvhead = blockIdx.x / p.row_blocks;
+  const int rb = blockIdx.x % p.row_blocks;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int row = rb * kRows + wave * 16 + c16;
+  const int64_t slot0 = ((int64_t)(kvhead * p.row_blocks + rb) * p.chunks) * 4 + wave;
+  float mmax = -INFINITY;
+  for (int c = 0; c < p.chunks; ++c) mmax = fmaxf(mmax, p.stats[(slot0 + 4 * c) * 128 + lane * 2]);
+  const float base = mmax == -INFINITY ? 0.0f : mmax;
+  f32x4_t acc[kHD / 16];
+#pragma unroll
+  for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.0f;
+  for (int c = 0; c < p.chunks; ++c) {
+    const int64_t slot = slot0 + 4 * c;
+    const float w = exp2f(p.stats[slot * 128 + lane * 2] - base);
+    lsum += w * p.stats[slot * 128 + lane * 2 + 1];
+    const float* pp = p.part + slot * (kHD / 16) * 256 + lane * 4;
+#pragma unroll
+    for (int tt = 0; tt < kHD / 16; ++tt)
+      acc[tt] += w * *reinterpret_cast<const f32x4_t*>(pp + tt * 256);
+  }
+  if (row >= p.rows) return;
+  const int node = row % p.n;
+  const int head = kvhead * p.group + row / p.n;
+  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+  uint16_t* orow = p.out + (int64_t)node * p.out_stride + (int64_t)head * kHD + 4 * g;
+#pragma unroll
+  for (int tt = 0; tt < kHD / 16; ++tt) {
+    u32x2_t o;
+    o.x = pack_bf16(acc[tt][0] * inv, acc[tt][1] * inv);
+    o.y = pack_bf16(acc[tt][2] * inv, acc[tt][3] * inv);
+    *reinterpret_cast<u32x2_t*>(orow + 16 * tt) = o;
+  }
+}
+
+// Bit-pack a [N, N] bool mask (row stride in bytes) into [N, words] u64.
+__global__ void tm_tree_mask_pack_kernel(const uint8_t* __restrict__ mask, int n,
+                                         int64_t stride, int words,
+                                         uint64_t* __restrict__ bits) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * words) return;
+  const int row = i / words, w = i % words;
+  uint64_t b = 0;
+  for (int j = 0; j < 64 && w * 64 + j < n; ++j)
+    b |= (uint64_t)(mask[(int64_t)row * stride + w * 64 + j] != 0) << j;
+  bits[i] = b;
+}
+
+struct Plan {
+  int64_t row_blocks, chunks, chunk_len, pairs, groups, part_floats, stats_floats;
+};
+
+int make_plan(int64_t n, int64_t hq, int64_t kvh, int64_t seq_len, int64_t page_size,
+              int64_t chunk_keys, Plan* pl) {
+  const int64_t s_total = seq_len + n;
+  const int64_t rows = (hq / kvh) * n;
+  pl->row_blocks = (rows + kRows - 1) / kRows;
+  const int64_t base = kvh * pl->row_blocks;
+  int64_t len;
+  if (chunk_keys > 0) {
+    len = chunk_keys;
+  } else {
+    int64_t chunks = (kTargetGroups + base - 1) / base;
+    chunks = std::min<int64_t>(chunks, std::max<int64_t>(1, s_total / kMinChunk));
+    len = (s_total + chunks - 1) / chunks;
+  }
+  len = (len + kKeys - 1) / kKeys * kKeys;
+  // the chunk's block-table entries must fit the LDS copy
+  const int64_t max_len = (int64_t)(kMaxPages - 2) * page_size / kKeys * kKeys;
+  if (max_len < kKeys) return TM_ERR_SHAPE;
+  len = std::min(len, max_len);
+  pl->chunk_len = len;
+  pl->chunks = (s_total + len - 1) / len;
+  pl->pairs = kvh * pl->chunks;
+  pl->groups = (pl->pairs + 7) / 8 * 8 * pl->row_blocks;
+  const int64_t slots = pl->chunks > 1 ? kvh * pl->row_blocks * pl->chunks * 4 : 0;
+  pl->part_floats = slots * (kHD / 16) * 256;
+  pl->stats_floats = slots * 128;
+  return TM_OK;
+}
+
+int check_shape(int64_t n, int64_t hq, int64_t kvh, int64_t hd, int64_t seq_len,
+                int64_t page_size) {
+  if (n < 1 || n > kMaxNodes || hd != kHD || kvh < 1 || hq < kvh || hq % kvh != 0 ||
+      hq > 1024 || seq_len < 0 || seq_len > (1 << 24))
+    return TM_ERR_SHAPE;
+  if (page_size < 1 || page_size > (1 << 16) || (page_size & (page_size - 1)) != 0)
+    return TM_ERR_SHAPE;
+  return TM_OK;
+}
+
+}  // namespace
+
+extern "C" int tm_tree_attention_plan(int64_t N, int64_t Hq, int64_t kvh, int64_t hd,
+                                      int64_t seq_len, int64_t page_size, int64_t chunk_keys,
+                                      int64_t* chunks, int64_t* workspace_bytes) {
+  int rc = check_shape(N, Hq, kvh, hd, seq_len, page_size);
+  if (rc) return rc;
+  if (chunk_keys < 0) return TM_ERR_ARG;
+  Plan pl;
+  rc = make_plan(N, Hq, kvh, seq_len, page_size, chunk_keys, &pl);
+  if (rc) return rc;
+  if (chunks) *chunks = pl.chunks;
+  if (workspace_bytes) *workspace_bytes = (pl.part_floats + pl.stats_floats) * 4;
+  return TM_OK;
+}
+
+extern "C" int tm_tree_mask_pack(const uint8_t* mask, int64_t N, int64_t row_stride,
+                                 uint64_t* bits, void* stream) {
+  if (N < 1 || N > kMaxNodes || row_stride < N) return TM_ERR_SHAPE;
+  if (((uintptr_t)bits % 8) != 0) return TM_ERR_ALIGN;
+  const int words = (int)((N + 63) / 64);
+  const int total = (int)N * words;
+  hipLaunchKernelGGL(tm_tree_mask_pack_kernel, dim3((total + 255) / 256), dim3(256), 0,
+                     (hipStream_t)stream, mask, (int)N, row_stride, words, bits);
+  TM_HIP_CHECK_LAUNCH();
+  return TM_OK;
+}
+
+extern "C" int tm_tree_attention(const void* q, int64_t q_stride, const void* k_tail,
+                                 const void* v_tail, int64_t tail_stride, void* k_cache,
+                                 void* v_cache, int64_t stride_page, int64_t stride_slot,
+                                 int64_t page_size, const int32_t* block_table,
+                                 int64_t num_table_pages, int64_t seq_len,
+                                 const int32_t* scratch_pages, int64_t num_scratch_pages,
+                                 int write_tree, const uint64_t* mask_bits, int64_t N,
+                                 int64_t Hq, int64_t kvh, int64_t hd, float scale, void* out,
+                                 int64_t out_stride, int64_t chunk_keys, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  int rc = check_shape(N, Hq, kvh, hd, seq_len, page_size);
+  if (rc) return rc;
+  if (chunk_keys < 0 || !(scale > 0.0f)) return TM_ERR_ARG;
+  if (q_stride < Hq * hd || tail_stride < kvh * hd || out_stride < Hq * hd ||
+      stride_slot < kvh * hd || stride_page < page_size * stride_slot)
+    return TM_ERR_SHAPE;
+  if ((seq_len + page_size - 1) / page_size > num_table_pages) return TM_ERR_SHAPE;
+  if (write_tree && (N + page_size - 1) / page_size > num_scratch_pages) return TM_ERR_SHAPE;
+  // 16-byte vectors everywhere: base pointers and strides in whole vectors
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)k_tail | (uintptr_t)v_tail |
+                          (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out;
+  if ((align % 16) != 0 || (q_stride % 8) || (tail_stride % 8) || (out_stride % 8) ||
+      (stride_page % 8) || (stride_slot % 8) || ((uintptr_t)mask_bits % 8) ||
+      ((uintptr_t)workspace % 16))
+    return TM_ERR_ALIGN;
+  Plan pl;
+  rc = make_plan(N, Hq, kvh, seq_len, page_size, chunk_keys, &pl);
+  if (rc) return rc;
+  if ((pl.part_floats + pl.stats_floats) * 4 > workspace_bytes) return TM_ERR_SHAPE;
+  if (pl.groups > INT32_MAX) return TM_ERR_SHAPE;
+
+  AttnParams p;
+  p.q = (const uint16_t*)q;
+  p.k_tail = (const uint16_t*)k_tail;
+  p.v_tail = (const uint16_t*)v_tail;
+  p.k_cache = (uint16_t*)k_cache;
+  p.v_cache = (uint16_t*)v_cache;
+  p.block_table = block_table;
+  p.scratch_pages = scratch_pages;
+  p.mask_bits = mask_bits;
+  p.out = (uint16_t*)out;
+  p.part = (float*)workspace;
+  p.stats = (float*)workspace + pl.part_floats;
+  p.q_stride = q_stride;
+  p.tail_stride = tail_stride;
+  p.out_stride = out_stride;
+  p.stride_page = stride_page;
+  p.stride_slot = stride_slot;
+  int shift = 0;
+  while ((int64_t(1) << shift) < page_size) ++shift;
+  p.page_shift = shift;
+  p.seq_len = (int)seq_len;
+  p.n = (int)N;
+  p.hq = (int)Hq;
+  p.kvh = (int)kvh;
+  p.group = (int)(Hq / kvh);
+  p.rows = (int)(p.group * N);
+  p.row_blocks = (int)pl.row_blocks;
+  p.chunks = (int)pl.chunks;
+  p.chunk_len = (int)pl.chunk_len;
+  p.pairs = (int)pl.pairs;
+  p.mask_words = (int)((N + 63) / 64);
+  p.write_tree = write_tree ? 1 : 0;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(tm_tree_attn_kernel, dim3((unsigned)pl.groups), dim3(kThreads), 0,
+                     (hipStream_t)stream, p);
+  TM_HIP_CHECK_LAUNCH();
+  if (pl.chunks > 1) {
+    hipLaunchKernelGGL(tm_tree_attn_combine_kernel, dim3((unsigned)(kvh * pl.row_blocks)),
+                       dim3(kThreads), 0, (hipStream_t)stream, p);
+    TM_HIP_CHECK_LAUNCH();
+  }
+  return TM_OK;
+}
