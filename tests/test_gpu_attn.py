@@ -80,6 +80,29 @@ def test_matches_oracle(n, hq, kvh, seq_len, page, chunk_keys):
     _check(out, _oracle(kv, q, k, v, mask, 1))
 
 
+@pytest.mark.parametrize("n,seq_len", [(64, 0), (7, 0), (64, 100), (16, 100)])
+def test_structured_masks(n, seq_len):
+    """Whole stages of tree keys (seq_len = 0: every key is a tree row), with
+    all-visible, self-only, causal, ancestor and root-plus-self masks; with
+    no prefix a self-only mask returns exactly the node's own V."""
+    _say(f"tree attention structured masks n={n} seq={seq_len}")
+    from treemoe_spec_amd.kernels.tree_attention import tree_attention
+
+    kv, q, k, v, anc = _case(n, 8, 2, seq_len, 16, 3)
+    eye = torch.eye(n, dtype=torch.bool)
+    masks = {"ones": torch.ones(n, n, dtype=torch.bool), "eye": eye,
+             "causal": torch.ones(n, n, dtype=torch.bool).tril(), "anc": anc,
+             "root": eye | torch.zeros(n, n, dtype=torch.bool).index_fill_(
+                 1, torch.tensor([0]), True)}
+    for name, m in masks.items():
+        out = tree_attention(q.cuda(), k.cuda(), v.cuda(), kv, 0, m.cuda())
+        torch.cuda.synchronize()
+        _check(out, _oracle(kv, q, k, v, m, 0))
+        if name == "eye" and seq_len == 0:
+            want = torch.stack([v[:, h // 4] for h in range(8)], 1).reshape(n, -1)
+            assert torch.equal(out.cpu(), want), name
+
+
 def test_write_tree_and_nothing_else():
     _say("tree attention write_tree bytes")
     from treemoe_spec_amd.kernels.tree_attention import tree_attention

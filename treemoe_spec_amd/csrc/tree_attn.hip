@@ -72,8 +72,13 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to packed bf16, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return (uint32_t)tm_f32_to_bf16(lo) | ((uint32_t)tm_f32_to_bf16(hi) << 16);
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // Stage layout: thread t stages keys 4 * quad + r (r = 0..3) at head-dim
@@ -85,35 +90,43 @@ struct Stage {
   u32x4_t v[4];
 };
 
+// The thread's 4 keys key0 .. key0 + 3 (key0 % 4 == 0) share one page
+// (page_size >= 4), so one block-table lookup serves them.  A stage that lies
+// entirely in the prefix takes the straight path; the chunk's boundary stages
+// pick each key's source (cache page, tree row, or zero past the chunk).
 __device__ __forceinline__ void load_stage(const AttnParams& p, const int* s_pages, int kb,
-                                           int c0, int c1, int kvhead, int quad, int part,
+                                           int c0, int c1, int64_t head_off, int quad,
                                            Stage& st) {
-  const int64_t head_off = (int64_t)kvhead * kHD + part * 8;
+  const int key0 = kb + 4 * quad;
+  const int pre_end = min(c1, p.seq_len);
+  const int pidx = key0 < pre_end ? (key0 >> p.page_shift) - (c0 >> p.page_shift) : 0;
+  const uint32_t page = (uint32_t)s_pages[pidx];
+  const int64_t cbase = (int64_t)((uint64_t)page * (uint64_t)p.stride_page) +
+                        (int64_t)(key0 & ((1 << p.page_shift) - 1)) * p.stride_slot + head_off;
+  if (kb + kKeys <= pre_end) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int key = kb + 4 * quad + r;
-    const bool valid = key < c1;
-    int64_t off;
-    const uint16_t* kb_ptr;
-    const uint16_t* vb_ptr;
-    if (valid && key < p.seq_len) {
-      // key < min(c1, seq_len): its page is among the chunk's staged entries
-      const int page = s_pages[(key >> p.page_shift) - (c0 >> p.page_shift)];
-      off = (int64_t)page * p.stride_page +
-            (int64_t)(key & ((1 << p.page_shift) - 1)) * p.stride_slot + head_off;
-      kb_ptr = p.k_cache;
-      vb_ptr = p.v_cache;
-    } else {
-      const int node = valid ? key - p.seq_len : 0;  // row 0 stands in past the end
-      off = (int64_t)node * p.tail_stride + head_off;
-      kb_ptr = p.k_tail;
-      vb_ptr = p.v_tail;
+    for (int r = 0; r < 4; ++r) {
+      const int64_t off = cbase + r * p.stride_slot;
+      st.k[r] = *reinterpret_cast<const u32x4_t*>(p.k_cache + off);
+      st.v[r] = *reinterpret_cast<const u32x4_t*>(p.v_cache + off);
     }
-    const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(kb_ptr + off);
-    const u32x4_t vv = *reinterpret_cast<const u32x4_t*>(vb_ptr + off);
-    const u32x4_t zero = {0u, 0u, 0u, 0u};
-    st.k[r] = valid ? kv : zero;
-    st.v[r] = valid ? vv : zero;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = key0 + r;
+      const bool in_pre = key < pre_end;
+      const bool in_tail = key >= p.seq_len && key < c1;
+      const int node = in_tail ? key - p.seq_len : 0;  // tree row 0 stands in otherwise
+      const int64_t off = in_pre ? cbase + r * p.stride_slot
+                                 : (int64_t)node * p.tail_stride + head_off;
+      const uint16_t* kp = in_pre ? p.k_cache : p.k_tail;
+      const uint16_t* vp = in_pre ? p.v_cache : p.v_tail;
+      const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(kp + off);
+      const u32x4_t vv = *reinterpret_cast<const u32x4_t*>(vp + off);
+      const u32x4_t zero = {0u, 0u, 0u, 0u};
+      st.k[r] = (in_pre || in_tail) ? kv : zero;
+      st.v[r] = (in_pre || in_tail) ? vv : zero;
+    }
   }
 }
 
@@ -153,6 +166,7 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
   const int c1 = min(c0 + p.chunk_len, s_total);
   const int quad = (tid & 3) + 4 * (tid >> 6);
   const int part = (tid >> 2) & 15;
+  const int64_t head_off = (int64_t)kvhead * kHD + part * 8;
 
   // tree rows of this KV head into the scratch pages (one workgroup per head)
   if (p.write_tree && rb == 0 && chunk == p.chunks - 1) {
@@ -199,7 +213,7 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
   __syncthreads();  // s_pages
 
   Stage st;
-  load_stage(p, s_pages, c0, c0, c1, kvhead, quad, part, st);
+  load_stage(p, s_pages, c0, c0, c1, head_off, quad, st);
   store_stage(s_buf, quad, part, st);
   __syncthreads();
 
@@ -214,7 +228,7 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
     // next stage's loads go out before this stage's MFMAs (the last stage
     // reloads itself: unconditional, so the wait counts stay exact)
     const int kn = c0 + min(s + 1, nstage - 1) * kKeys;
-    load_stage(p, s_pages, kn, c0, c1, kvhead, quad, part, st);
+    load_stage(p, s_pages, kn, c0, c1, head_off, quad, st);
 
     const uint8_t* kl = s_buf + (s & 1) * kStage;
     const uint8_t* vl = kl + kKBytes;
@@ -230,47 +244,58 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
         sc[t] = mfma16(a, qf[ks], sc[t]);
       }
     }
-    // scale, mask, running max
-    const bool all_visible = kb + kKeys <= min(c1, p.seq_len);
+    // tree and chunk-end masking (boundary stages only)
+    if (!(kb + kKeys <= min(c1, p.seq_len))) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // integer and/or, no short-circuit: the visibility is a plain
+          // select, with no divergent branch around the accumulator copy
+          const int key = kb + 16 * t + 4 * g + i;
+          const int j = key - p.seq_len;
+          uint64_t word = mw[0];
+          word = j >= 64 ? mw[1] : word;
+          word = j >= 128 ? mw[2] : word;
+          word = j >= 192 ? mw[3] : word;
+          const uint32_t bit = (uint32_t)(word >> (j & 63)) & 1u;
+          const uint32_t vis = (uint32_t)(key < c1) & ((uint32_t)(j < 0) | bit);
+          sc[t][i] = vis ? sc[t][i] : -INFINITY;
+        }
+      }
+    }
+    // running max in base 2: max(scale * s) = scale * max(s) for scale > 0
     float mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v = sc[t][i] * p.scale_log2;
-        if (!all_visible) {
-          const int key = kb + 16 * t + 4 * g + i;
-          bool vis = key < c1;
-          if (key >= p.seq_len) {
-            const int j = key - p.seq_len;
-            const uint64_t word = j < 64 ? mw[0] : j < 128 ? mw[1] : j < 192 ? mw[2] : mw[3];
-            vis = vis && ((word >> (j & 63)) & 1u);
-          }
-          v = vis ? v : -INFINITY;
-        }
-        sc[t][i] = v;
-        mx = fmaxf(mx, v);
-      }
-    }
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[t][i]);
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float base = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f(m_run - base);
-    m_run = m_new;
-    float lsum = 0.0f;
+    const float cand = mx * p.scale_log2;
+    // The reference point moves only when the stage maximum exceeds it by more
+    // than 2^8 (weights stay <= 256), so the accumulators are rescaled rarely;
+    // the final division by the sum taken against the same reference makes
+    // this exact in real arithmetic.
+    const bool bump = cand > m_run + 8.0f;
+    if (__any(bump)) {
+      const float m_use = bump ? cand : m_run;
+      const float alpha = bump ? exp2f(m_run - m_use) : 1.0f;
+#pragma unroll
+      for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] *= alpha;
+      l_run *= alpha;
+      m_run = m_use;
+    }
+    const float neg_base = m_run == -INFINITY ? 0.0f : -m_run;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = exp2f(sc[t][i] - base);
+        const float e = __builtin_amdgcn_exp2f(fmaf(sc[t][i], p.scale_log2, neg_base));
         sc[t][i] = e;
-        lsum += e;
+        l_run += e;
       }
     }
-    l_run = l_run * alpha + lsum;
-#pragma unroll
-    for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] *= alpha;
     // O^T += V^T P^T over two 32-key k-steps
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {
@@ -319,43 +344,46 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
   sp[1] = l_run;
 }
 
-// One workgroup per (KV head, row block): O = sum_c w_c O_c / sum_c w_c l_c
-// with w_c = 2^(m_c - max m), chunks in order.
+// One thread per (KV head, row block, wave, 16-column head-dim tile, lane):
+// merges that lane's chunk partials in chunk order with a running maximum,
+//   M' = max(M, m_c),  O = O 2^(M - M') + O_c 2^(m_c - M'),  L likewise,
+// then writes O / L.  Branch-free, so the loads of later chunks can issue early.
 __global__ void __launch_bounds__(kThreads) tm_tree_attn_combine_kernel(AttnParams p) {
-  const int kvhead = blockIdx.x / p.row_blocks;
-  const int rb = blockIdx.x % p.row_blocks;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, c16 = lane & 15;
-  const int row = rb * kRows + wave * 16 + c16;
-  const int64_t slot0 = ((int64_t)(kvhead * p.row_blocks + rb) * p.chunks) * 4 + wave;
-  float mmax = -INFINITY;
-  for (int c = 0; c < p.chunks; ++c) mmax = fmaxf(mmax, p.stats[(slot0 + 4 * c) * 128 + lane * 2]);
-  const float base = mmax == -INFINITY ? 0.0f : mmax;
-  f32x4_t acc[kHD / 16];
-#pragma unroll
-  for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.0f;
+  const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int lane = (int)(u & 63);
+  const int tt = (int)((u >> 6) & (kHD / 16 - 1));
+  const int64_t kw = u >> 9;                  // (kvhead * row_blocks + rb) * 4 + wave
+  const int wave = (int)(kw & 3);
+  const int64_t kr = kw >> 2;                 // kvhead * row_blocks + rb
+  if (kr >= (int64_t)p.kvh * p.row_blocks) return;
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
   for (int c = 0; c < p.chunks; ++c) {
-    const int64_t slot = slot0 + 4 * c;
-    const float w = exp2f(p.stats[slot * 128 + lane * 2] - base);
-    lsum += w * p.stats[slot * 128 + lane * 2 + 1];
-    const float* pp = p.part + slot * (kHD / 16) * 256 + lane * 4;
-#pragma unroll
-    for (int tt = 0; tt < kHD / 16; ++tt)
-      acc[tt] += w * *reinterpret_cast<const f32x4_t*>(pp + tt * 256);
+    const int64_t slot = (kr * p.chunks + c) * 4 + wave;
+    const f32x2_t st = *reinterpret_cast<const f32x2_t*>(p.stats + slot * 128 + lane * 2);
+    const f32x4_t oc =
+        *reinterpret_cast<const f32x4_t*>(p.part + slot * (kHD / 16) * 256 + tt * 256 + lane * 4);
+    const float mn = fmaxf(m_run, st.x);
+    const float ref = mn == -INFINITY ? 0.0f : mn;
+    const float a = exp2f(m_run - ref);       // 0 while nothing was visible
+    const float b = exp2f(st.x - ref);
+    l_run = l_run * a + st.y * b;
+    o = o * a + oc * b;
+    m_run = mn;
   }
+  const int rb = (int)(kr % p.row_blocks);
+  const int kvhead = (int)(kr / p.row_blocks);
+  const int row = rb * kRows + wave * 16 + (lane & 15);
   if (row >= p.rows) return;
   const int node = row % p.n;
   const int head = kvhead * p.group + row / p.n;
-  const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-  uint16_t* orow = p.out + (int64_t)node * p.out_stride + (int64_t)head * kHD + 4 * g;
-#pragma unroll
-  for (int tt = 0; tt < kHD / 16; ++tt) {
-    u32x2_t o;
-    o.x = pack_bf16(acc[tt][0] * inv, acc[tt][1] * inv);
-    o.y = pack_bf16(acc[tt][2] * inv, acc[tt][3] * inv);
-    *reinterpret_cast<u32x2_t*>(orow + 16 * tt) = o;
-  }
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  u32x2_t w;
+  w.x = pack_bf16(o[0] * inv, o[1] * inv);
+  w.y = pack_bf16(o[2] * inv, o[3] * inv);
+  *reinterpret_cast<u32x2_t*>(p.out + (int64_t)node * p.out_stride + (int64_t)head * kHD +
+                              16 * tt + 4 * (lane >> 4)) = w;
 }
 
 // Bit-pack a [N, N] bool mask (row stride in bytes) into [N, words] u64.
@@ -409,7 +437,7 @@ int check_shape(int64_t n, int64_t hq, int64_t kvh, int64_t hd, int64_t seq_len,
   if (n < 1 || n > kMaxNodes || hd != kHD || kvh < 1 || hq < kvh || hq % kvh != 0 ||
       hq > 1024 || seq_len < 0 || seq_len > (1 << 24))
     return TM_ERR_SHAPE;
-  if (page_size < 1 || page_size > (1 << 16) || (page_size & (page_size - 1)) != 0)
+  if (page_size < 4 || page_size > (1 << 16) || (page_size & (page_size - 1)) != 0)
     return TM_ERR_SHAPE;
   return TM_OK;
 }
@@ -510,7 +538,9 @@ extern "C" int tm_tree_attention(const void* q, int64_t q_stride, const void* k_
                      (hipStream_t)stream, p);
   TM_HIP_CHECK_LAUNCH();
   if (pl.chunks > 1) {
-    hipLaunchKernelGGL(tm_tree_attn_combine_kernel, dim3((unsigned)(kvh * pl.row_blocks)),
+    // kvh * row_blocks * 4 waves * 8 tiles * 64 lanes threads
+    hipLaunchKernelGGL(tm_tree_attn_combine_kernel,
+                       dim3((unsigned)(kvh * pl.row_blocks * 4 * (kHD / 16) * 64 / kThreads)),
                        dim3(kThreads), 0, (hipStream_t)stream, p);
     TM_HIP_CHECK_LAUNCH();
   }
