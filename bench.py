@@ -318,7 +318,83 @@ def secondary(m, inp2, args) -> dict:
                                         "us_device": round(dev_ms * 1e3, 2),
                                         "gbs_device": round(b / (dev_ms * 1e-3) / 1e9, 1),
                                         "accepted": num, "bytes_alg": b}
+    out["config4_tree_attention"] = tree_attention_secondary(reps)
     return out
+
+
+def tree_attention_secondary(reps: int) -> dict:
+    """The verification forward's attention at the config-4 cache shape: a
+    64-node tree (random parents, depth <= 8), 32 query heads over 8 KV heads,
+    head dim 128, page 16, 4096 committed positions, one layer.  Device time
+    of the C-ABI call (mask packed and tables resident), the CPU oracle on a
+    bounded sample beside it."""
+    import ctypes
+
+    import torch
+
+    from oracle import attn_ref
+    from treemoe_spec_amd import _capi
+    from treemoe_spec_amd.kernels import tree_attention as ta
+    from treemoe_spec_amd.kv_cache import MixtralConfig, PagedKVCache
+    from treemoe_spec_amd.workloads import random_tree
+
+    log("secondary tree attention config 4")
+    n, hq, kvh, hd, seq, page = 64, 32, 8, 128, 4096, 16
+    g = torch.Generator().manual_seed(4)
+    cfg = MixtralConfig(num_layers=1)
+    kv = PagedKVCache(cfg, seq // page + 4 + 8, device="cuda", page_size=page, tree_size=n)
+    gd = torch.Generator(device="cuda").manual_seed(4)
+    kv.k.normal_(generator=gd)
+    kv.v.normal_(generator=gd)
+    kv._ensure_capacity(seq)
+    kv.seq_len = seq
+    q = torch.randn(n, hq, hd, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(n, kvh, hd, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn(n, kvh, hd, generator=g).to(torch.bfloat16).cuda()
+    parent, _, _, _ = random_tree(g, n, 8, 32000)
+    mask = attn_ref.ancestor_mask(parent).cuda()
+    out = ta.tree_attention(q, k, v, kv, 0, mask)
+    bits = ta.pack_tree_mask(mask)
+    table, scratch = kv.device_tables(q.device)
+    chunks, wbytes = ctypes.c_int64(), ctypes.c_int64()
+    _capi.call("tm_tree_attention_plan", n, hq, kvh, hd, seq, page, 0, ctypes.byref(chunks),
+               ctypes.byref(wbytes))
+    ws = torch.empty(max(wbytes.value, 16), dtype=torch.uint8, device="cuda")
+    kc, vc = kv.k[0], kv.v[0]
+    stream = _capi.stream_of(q.device)
+    args = (q.data_ptr(), hq * hd, k.data_ptr(), v.data_ptr(), kvh * hd, kc.data_ptr(),
+            vc.data_ptr(), kc.stride(0), kc.stride(1), page, table.data_ptr(),
+            len(kv.block_table), seq, scratch.data_ptr(), len(kv.tree_pages), 1,
+            bits.data_ptr(), n, hq, kvh, hd, hd ** -0.5, out.data_ptr(), hq * hd, 0,
+            ws.data_ptr(), wbytes.value, stream)
+    fn = _capi.lib().tm_tree_attention
+
+    def step():
+        rc = fn(*args)
+        if rc:
+            raise RuntimeError(f"tm_tree_attention status {rc}")
+
+    for _ in range(5):
+        step()
+    dev_ms = events_time_ms(step, max(reps, 50))
+    bytes_alg = (2 * seq * kvh * hd * 2          # prefix K and V, read once
+                 + 2 * 2 * n * kvh * hd * 2      # tree K and V read, and stored to scratch
+                 + 2 * n * hq * hd * 2)          # q in, context out
+    flops = 4 * n * hq * (seq + n) * hd          # QK^T and PV over every key, masked or not
+    # CPU: the oracle (float32 restatement of gather + mask + SDPA) on the host
+    kc_cpu, vc_cpu = kv.k.cpu(), kv.v.cpu()
+    qc, kt, vt, mc = q.cpu(), k.cpu(), v.cpu(), mask.cpu()
+    t0 = time.perf_counter()
+    attn_ref.tree_attention(qc, kt, vt, kc_cpu, vc_cpu, 0, kv.block_table, seq, page, mc)
+    cpu_ms = (time.perf_counter() - t0) * 1e3
+    return {"us_device": round(dev_ms * 1e3, 2), "chunks": chunks.value,
+            "gbs": round(bytes_alg / (dev_ms * 1e-3) / 1e9, 1),
+            "pct_hbm_peak": round(100 * bytes_alg / (dev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+            "tflops": round(flops / (dev_ms * 1e-3) / 1e12, 2),
+            "pct_mfma_peak": round(100 * flops / (dev_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                                   2),
+            "bytes_alg": bytes_alg, "flops": flops,
+            "cpu_oracle_ms": round(cpu_ms, 2), "cpu_threads": torch.get_num_threads()}
 
 
 if __name__ == "__main__":

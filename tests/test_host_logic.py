@@ -141,3 +141,48 @@ def test_workloads_are_seeded():
     for node, kids in enumerate(w1.children):
         toks = [int(w1.tokens[c]) for c in kids]
         assert len(toks) == len(set(toks)) and all(c > node for c in kids)
+
+
+def test_moe_adapter_host_logic(monkeypatch):
+    """The engine hook's host logic (benchmarks/bench_e2e.py:482-504, 654-658):
+    accept from current_accept_prob when it matches the row count, else ones;
+    the layer's budget from current_layer_budgets, else the default; the
+    demand handed to the observer; the routing reused by the GEMMs."""
+    from types import SimpleNamespace
+
+    import treemoe_spec_amd.moe_adapter as ad
+
+    calls = []
+    routing = SimpleNamespace(demand=torch.tensor([3.0, 1.0]))
+
+    def fake_route(x, router, accept, budget, inter, top1_threshold, routing_objective):
+        calls.append(("route", accept.clone(), budget, inter, top1_threshold,
+                      routing_objective))
+        return routing
+
+    def fake_forward(x, w1, w2, w3, router, accept, budget, routing=None, deterministic=True):
+        calls.append(("forward", budget, routing, deterministic))
+        return x + 1
+
+    monkeypatch.setattr(ad, "route_experts", fake_route)
+    monkeypatch.setattr(ad, "tree_moe_forward", fake_forward)
+    fn = ad.make_moe_fn(expert_budget=6, top1_threshold=0.1, routing_objective="critical_path",
+                        deterministic=False, tree_size=4, device="cpu")
+    lw = SimpleNamespace(router=None, w1=torch.zeros(2, 24, 8), w2=None, w3=None)
+    x = torch.zeros(4, 8)
+    assert torch.equal(fn.current_accept_prob, torch.ones(4))
+    fn.current_accept_prob = torch.tensor([0.9, 0.5, 0.2, 0.01])
+    seen = []
+    fn.demand_observer = lambda li, d: seen.append((li, d))
+    out = fn(x, lw, 1)
+    assert torch.equal(out, x + 1)
+    kind, accept, budget, inter, tau, objective = calls[0]
+    assert torch.equal(accept, torch.tensor([0.9, 0.5, 0.2, 0.01]))
+    assert (budget, inter, tau, objective) == (6, 24, 0.1, "critical_path")
+    assert calls[1] == ("forward", 6, routing, False)
+    assert seen == [(1, routing.demand)]
+    # per-layer budgets and a row count that differs from the tree
+    fn.current_layer_budgets = torch.tensor([8, 3])
+    calls.clear()
+    fn(torch.zeros(3, 8), lw, 1)
+    assert torch.equal(calls[0][1], torch.ones(3)) and calls[0][2] == 3
