@@ -7,24 +7,24 @@
 //
 // Work decomposition.  For one KV head the group * N query rows (rows ordered
 // head-in-group major, node minor) share every K/V byte, so a workgroup takes
-// 64 of those rows (4 waves x 16) against one chunk of keys; the K/V of the
+// 128 of those rows (4 waves x 32) against one chunk of keys; the K/V of the
 // chunk is staged through LDS 64 keys at a time and each key byte is read from
 // HBM once per (KV head, chunk), by the row blocks of that pair, which are
 // launched on one XCD (launch indices congruent mod 8) so they share its L2.
 //
-// Per wave and 64-key stage (v_mfma_f32_16x16x32_bf16 throughout):
-//   S^T = K Q^T    A = K rows from LDS, B = Q^T held in registers,
-//                  lane l gets S^T[key 16t + 4(l/16) + i][query l%16];
-//   online softmax in base 2, per query (= per lane column), the 4 lanes of a
-//                  query combined by two xor shuffles;
-//   O^T += V^T P^T B = P^T straight from the S^T registers: the MFMA's k slots
-//                  8(l/16) + j are mapped to keys 32s + 4(l/16) + j (j < 4) and
-//                  32s + 16 + 4(l/16) + j - 4, which are exactly the keys the
-//                  lane holds; A = V^T read with the same key map from a
-//                  transposed copy of V in LDS.
-// A chunk's unnormalised O^T, running max and sum go to a workspace and a
-// second kernel combines the chunks in chunk order (deterministic); with one
-// chunk the first kernel writes the normalised output itself.
+// Per wave and 64-key stage (v_mfma_f32_32x32x16_bf16 throughout):
+//   S^T = K Q^T    A = K rows from LDS, B = Q^T held in registers, two 32-key
+//                  tiles; lane l gets S^T[key 32t + 8(v/4) + 4(l/32) + v%4]
+//                  [query l%32] in accumulator value v;
+//   online softmax in base 2, per query (= per lane column), the 2 lanes of a
+//                  query combined by one xor shuffle;
+//   O^T += V^T P^T B = P^T straight from the S^T registers: the MFMA's k slot j
+//                  of k-step (t, m) is mapped to key 32t + 16m + 8(j/4) +
+//                  4(l/32) + j%4, the lane's own value 8m + j; A = V^T read with
+//                  the same key map from a transposed copy of V in LDS.
+// A chunk's normalised O^T (fp16), reference maximum and sum go to a workspace
+// and a second kernel combines the chunks in chunk order (deterministic); with
+// one chunk the first kernel writes the output itself.
 #include <algorithm>
 #include <cmath>
 
@@ -34,7 +34,7 @@ namespace {
 
 constexpr int kHD = 128;                    // head dim
 constexpr int kThreads = 256;               // 4 waves
-constexpr int kRows = 64;                   // query rows per workgroup
+constexpr int kRows = 128;                  // query rows per workgroup (4 waves x 32)
 constexpr int kKeys = 64;                   // keys per LDS stage
 constexpr int kKStride = kHD * 2 + 16;      // bytes per K row in LDS (272)
 constexpr int kVStride = kKeys * 2 + 8;     // bytes per V^T row in LDS (136)
@@ -66,11 +66,6 @@ struct AttnParams {
   int mask_words, write_tree;
   float scale_log2;
 };
-
-__device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -149,6 +144,21 @@ __device__ __forceinline__ void store_stage(uint8_t* buf, int quad, int part, co
   }
 }
 
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+
+// 32x32x16 bf16 MFMA.  Lane l: A row l%32 and B column l%32, k 8(l/32) .. +7;
+// accumulator value v is C[8(v/4) + 4(l/32) + v%4][l%32].
+__device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Partials of one (workgroup slot, wave): 16 groups x 64 lanes x 4 fp16 of
+// the chunk's normalised O^T, and (m, l) per query (32 float2).
+constexpr int kPartHalves = (kHD / 32) * 16 * 64;  // 4096 per wave slot
+constexpr int kStatFloats = 64;                      // 32 queries x (m, l)
+
 __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_buf[2 * kStage];
   __shared__ int s_pages[kMaxPages];
@@ -160,7 +170,7 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
   const int kvhead = pair / p.chunks;
   const int chunk = pair % p.chunks;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int g = lane >> 4, c16 = lane & 15;
+  const int half = lane >> 5, c32 = lane & 31;
   const int s_total = p.seq_len + p.n;
   const int c0 = chunk * p.chunk_len;
   const int c1 = min(c0 + p.chunk_len, s_total);
@@ -189,17 +199,17 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
   for (int i = tid; i < npages; i += kThreads)
     s_pages[i] = p.block_table[(c0 >> p.page_shift) + i];
 
-  // this lane's query row: Q^T fragments and the tree-mask row
-  const int row = rb * kRows + wave * 16 + c16;
+  // this lane's query (column c32 of the wave's 32): Q^T fragments, mask row
+  const int row = rb * kRows + wave * 32 + c32;
   const bool row_ok = row < p.rows;
   const int node = row_ok ? row % p.n : 0;
   const int head = kvhead * p.group + (row_ok ? row / p.n : 0);
-  u32x4_t qf[kHD / 32];
+  u32x4_t qf[kHD / 16];
   {
-    const uint16_t* qrow = p.q + (int64_t)node * p.q_stride + (int64_t)head * kHD + 8 * g;
+    const uint16_t* qrow = p.q + (int64_t)node * p.q_stride + (int64_t)head * kHD + 8 * half;
 #pragma unroll
-    for (int ks = 0; ks < kHD / 32; ++ks) {
-      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + 32 * ks);
+    for (int ks = 0; ks < kHD / 16; ++ks) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + 16 * ks);
       const u32x4_t zero = {0u, 0u, 0u, 0u};
       qf[ks] = row_ok ? v : zero;
     }
@@ -217,9 +227,11 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
   store_stage(s_buf, quad, part, st);
   __syncthreads();
 
-  f32x4_t acc[kHD / 16];
+  f32x16_t acc[kHD / 32];
 #pragma unroll
-  for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int ht = 0; ht < kHD / 32; ++ht)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[ht][v] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
   const int nstage = (c1 - c0 + kKeys - 1) / kKeys;
@@ -232,27 +244,28 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
 
     const uint8_t* kl = s_buf + (s & 1) * kStage;
     const uint8_t* vl = kl + kKBytes;
-    // S^T tiles: keys 16t .. 16t+15 of the stage
-    f32x4_t sc[4];
+    // S^T = K Q^T over two 32-key tiles; lane holds keys
+    // 32 kt + 8 (v/4) + 4 half + v%4 of query c32 in sc[kt][v]
+    f32x16_t sc[2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      sc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-      for (int ks = 0; ks < kHD / 32; ++ks) {
-        const u32x4_t a =
-            *reinterpret_cast<const u32x4_t*>(kl + (16 * t + c16) * kKStride + ks * 64 + g * 16);
-        sc[t] = mfma16(a, qf[ks], sc[t]);
+      for (int v = 0; v < 16; ++v) sc[kt][v] = 0.0f;
+#pragma unroll
+      for (int ks = 0; ks < kHD / 16; ++ks) {
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(
+            kl + (32 * kt + c32) * kKStride + ks * 32 + half * 16);
+        sc[kt] = mfma32(a, qf[ks], sc[kt]);
       }
     }
-    // tree and chunk-end masking (boundary stages only)
+    // tree and chunk-end masking (boundary stages only); integer and/or, so
+    // the visibility is a plain select
     if (!(kb + kKeys <= min(c1, p.seq_len))) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
+      for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          // integer and/or, no short-circuit: the visibility is a plain
-          // select, with no divergent branch around the accumulator copy
-          const int key = kb + 16 * t + 4 * g + i;
+        for (int v = 0; v < 16; ++v) {
+          const int key = kb + 32 * kt + 8 * (v >> 2) + 4 * half + (v & 3);
           const int j = key - p.seq_len;
           uint64_t word = mw[0];
           word = j >= 64 ? mw[1] : word;
@@ -260,17 +273,17 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
           word = j >= 192 ? mw[3] : word;
           const uint32_t bit = (uint32_t)(word >> (j & 63)) & 1u;
           const uint32_t vis = (uint32_t)(key < c1) & ((uint32_t)(j < 0) | bit);
-          sc[t][i] = vis ? sc[t][i] : -INFINITY;
+          sc[kt][v] = vis ? sc[kt][v] : -INFINITY;
         }
       }
     }
-    // running max in base 2: max(scale * s) = scale * max(s) for scale > 0
+    // running max in base 2 (scale > 0 commutes with max); the query's other
+    // 32 keys of the stage sit in lane c32 ^ 32
     float mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[t][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[kt][v]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float cand = mx * p.scale_log2;
     // The reference point moves only when the stage maximum exceeds it by more
@@ -282,108 +295,133 @@ __global__ void __launch_bounds__(kThreads) tm_tree_attn_kernel(AttnParams p) {
       const float m_use = bump ? cand : m_run;
       const float alpha = bump ? exp2f(m_run - m_use) : 1.0f;
 #pragma unroll
-      for (int tt = 0; tt < kHD / 16; ++tt) acc[tt] *= alpha;
+      for (int ht = 0; ht < kHD / 32; ++ht) acc[ht] *= alpha;
       l_run *= alpha;
       m_run = m_use;
     }
     const float neg_base = m_run == -INFINITY ? 0.0f : -m_run;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(sc[t][i], p.scale_log2, neg_base));
-        sc[t][i] = e;
+      for (int v = 0; v < 16; ++v) {
+        const float e = __builtin_amdgcn_exp2f(fmaf(sc[kt][v], p.scale_log2, neg_base));
+        sc[kt][v] = e;
         l_run += e;
       }
     }
-    // O^T += V^T P^T over two 32-key k-steps
+    // O^T += V^T P^T: k-step (kt, m) covers keys 32 kt + 16 m + [0, 16); its
+    // k slot j of lane half h is key 32 kt + 16 m + 8 (j/4) + 4 h + j%4, which
+    // is the lane's own value sc[kt][8 m + j]
 #pragma unroll
-    for (int k2 = 0; k2 < 2; ++k2) {
-      u32x4_t b;
-      b.x = pack_bf16(sc[2 * k2][0], sc[2 * k2][1]);
-      b.y = pack_bf16(sc[2 * k2][2], sc[2 * k2][3]);
-      b.z = pack_bf16(sc[2 * k2 + 1][0], sc[2 * k2 + 1][1]);
-      b.w = pack_bf16(sc[2 * k2 + 1][2], sc[2 * k2 + 1][3]);
+    for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-      for (int tt = 0; tt < kHD / 16; ++tt) {
-        const uint8_t* vr = vl + (16 * tt + c16) * kVStride + (32 * k2 + 4 * g) * 2;
-        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
-        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 32);
-        const u32x4_t a = {lo.x, lo.y, hi.x, hi.y};
-        acc[tt] = mfma16(a, b, acc[tt]);
+      for (int m = 0; m < 2; ++m) {
+        u32x4_t b;
+        b.x = pack_bf16(sc[kt][8 * m + 0], sc[kt][8 * m + 1]);
+        b.y = pack_bf16(sc[kt][8 * m + 2], sc[kt][8 * m + 3]);
+        b.z = pack_bf16(sc[kt][8 * m + 4], sc[kt][8 * m + 5]);
+        b.w = pack_bf16(sc[kt][8 * m + 6], sc[kt][8 * m + 7]);
+#pragma unroll
+        for (int ht = 0; ht < kHD / 32; ++ht) {
+          const uint8_t* vr = vl + (32 * ht + c32) * kVStride + (32 * kt + 16 * m + 4 * half) * 2;
+          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
+          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 16);
+          const u32x4_t a = {lo.x, lo.y, hi.x, hi.y};
+          acc[ht] = mfma32(a, b, acc[ht]);
+        }
       }
     }
     store_stage(s_buf + ((s + 1) & 1) * kStage, quad, part, st);
     __syncthreads();
   }
 
-  // the 4 lanes of a query hold partial sums over disjoint keys
-  l_run += __shfl_xor(l_run, 16);
+  // the two lanes of a query hold partial sums over disjoint keys
   l_run += __shfl_xor(l_run, 32);
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
 
   if (p.chunks == 1) {
     if (row_ok) {
-      const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-      uint16_t* orow = p.out + (int64_t)node * p.out_stride + (int64_t)head * kHD + 4 * g;
+      uint16_t* orow = p.out + (int64_t)node * p.out_stride + (int64_t)head * kHD + 4 * half;
 #pragma unroll
-      for (int tt = 0; tt < kHD / 16; ++tt) {
-        u32x2_t o;
-        o.x = pack_bf16(acc[tt][0] * inv, acc[tt][1] * inv);
-        o.y = pack_bf16(acc[tt][2] * inv, acc[tt][3] * inv);
-        *reinterpret_cast<u32x2_t*>(orow + 16 * tt) = o;
+      for (int ht = 0; ht < kHD / 32; ++ht) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          u32x2_t o;
+          o.x = pack_bf16(acc[ht][4 * gq + 0] * inv, acc[ht][4 * gq + 1] * inv);
+          o.y = pack_bf16(acc[ht][4 * gq + 2] * inv, acc[ht][4 * gq + 3] * inv);
+          *reinterpret_cast<u32x2_t*>(orow + 32 * ht + 8 * gq) = o;
+        }
       }
     }
     return;
   }
+  // chunk partial: O^T / l in fp16 (|value| <= max |v|), and (m, l)
   const int64_t slot = ((int64_t)(kvhead * p.row_blocks + rb) * p.chunks + chunk) * 4 + wave;
-  float* pp = p.part + slot * (kHD / 16) * 256 + lane * 4;
+  _Float16* pp = reinterpret_cast<_Float16*>(p.part) + slot * kPartHalves + lane * 4;
 #pragma unroll
-  for (int tt = 0; tt < kHD / 16; ++tt) *reinterpret_cast<f32x4_t*>(pp + tt * 256) = acc[tt];
-  float* sp = p.stats + slot * 128 + lane * 2;
-  sp[0] = m_run;
-  sp[1] = l_run;
+  for (int ht = 0; ht < kHD / 32; ++ht) {
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      f16x4_t h;
+      h[0] = (_Float16)(acc[ht][4 * gq + 0] * inv);
+      h[1] = (_Float16)(acc[ht][4 * gq + 1] * inv);
+      h[2] = (_Float16)(acc[ht][4 * gq + 2] * inv);
+      h[3] = (_Float16)(acc[ht][4 * gq + 3] * inv);
+      *reinterpret_cast<f16x4_t*>(pp + (ht * 4 + gq) * 256) = h;
+    }
+  }
+  if (half == 0) {
+    f32x2_t st2 = {m_run, l_run};
+    *reinterpret_cast<f32x2_t*>(p.stats + slot * kStatFloats + c32 * 2) = st2;
+  }
 }
 
-// One thread per (KV head, row block, wave, 16-column head-dim tile, lane):
-// merges that lane's chunk partials in chunk order with a running maximum,
-//   M' = max(M, m_c),  O = O 2^(M - M') + O_c 2^(m_c - M'),  L likewise,
-// then writes O / L.  Branch-free, so the loads of later chunks can issue early.
+// One thread per (KV head, row block, wave, 4-value group, lane): merges the
+// chunks' normalised partials in chunk order with a running maximum,
+//   w_c = l_c 2^(m_c - M),  O = sum_c w_c O_c / sum_c w_c,
+// keeping the running sums against the running maximum.  Branch-free, so the
+// loads of later chunks can issue early.
 __global__ void __launch_bounds__(kThreads) tm_tree_attn_combine_kernel(AttnParams p) {
   const int64_t u = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   const int lane = (int)(u & 63);
-  const int tt = (int)((u >> 6) & (kHD / 16 - 1));
-  const int64_t kw = u >> 9;                  // (kvhead * row_blocks + rb) * 4 + wave
+  const int grp = (int)((u >> 6) & 15);       // (ht, gq) = (grp / 4, grp % 4)
+  const int64_t kw = u >> 10;                 // (kvhead * row_blocks + rb) * 4 + wave
   const int wave = (int)(kw & 3);
-  const int64_t kr = kw >> 2;                 // kvhead * row_blocks + rb
+  const int64_t kr = kw >> 2;
   if (kr >= (int64_t)p.kvh * p.row_blocks) return;
-  float m_run = -INFINITY, l_run = 0.0f;
+  const int c32 = lane & 31, half = lane >> 5;
+  float m_run = -INFINITY, w_sum = 0.0f;
   f32x4_t o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
   for (int c = 0; c < p.chunks; ++c) {
     const int64_t slot = (kr * p.chunks + c) * 4 + wave;
-    const f32x2_t st = *reinterpret_cast<const f32x2_t*>(p.stats + slot * 128 + lane * 2);
-    const f32x4_t oc =
-        *reinterpret_cast<const f32x4_t*>(p.part + slot * (kHD / 16) * 256 + tt * 256 + lane * 4);
+    const f32x2_t st = *reinterpret_cast<const f32x2_t*>(p.stats + slot * kStatFloats + c32 * 2);
+    const f16x4_t hc = *reinterpret_cast<const f16x4_t*>(
+        reinterpret_cast<const _Float16*>(p.part) + slot * kPartHalves + grp * 256 + lane * 4);
     const float mn = fmaxf(m_run, st.x);
     const float ref = mn == -INFINITY ? 0.0f : mn;
     const float a = exp2f(m_run - ref);       // 0 while nothing was visible
-    const float b = exp2f(st.x - ref);
-    l_run = l_run * a + st.y * b;
-    o = o * a + oc * b;
+    const float b = st.y * exp2f(st.x - ref);
+    w_sum = w_sum * a + b;
+    o[0] = o[0] * a + (float)hc[0] * b;
+    o[1] = o[1] * a + (float)hc[1] * b;
+    o[2] = o[2] * a + (float)hc[2] * b;
+    o[3] = o[3] * a + (float)hc[3] * b;
     m_run = mn;
   }
   const int rb = (int)(kr % p.row_blocks);
   const int kvhead = (int)(kr / p.row_blocks);
-  const int row = rb * kRows + wave * 16 + (lane & 15);
+  const int row = rb * kRows + wave * 32 + c32;
   if (row >= p.rows) return;
   const int node = row % p.n;
   const int head = kvhead * p.group + row / p.n;
-  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  const float inv = w_sum > 0.0f ? 1.0f / w_sum : 0.0f;
   u32x2_t w;
   w.x = pack_bf16(o[0] * inv, o[1] * inv);
   w.y = pack_bf16(o[2] * inv, o[3] * inv);
+  const int ht = grp >> 2, gq = grp & 3;
   *reinterpret_cast<u32x2_t*>(p.out + (int64_t)node * p.out_stride + (int64_t)head * kHD +
-                              16 * tt + 4 * (lane >> 4)) = w;
+                              32 * ht + 8 * gq + 4 * half) = w;
 }
 
 // Bit-pack a [N, N] bool mask (row stride in bytes) into [N, words] u64.
@@ -427,8 +465,8 @@ int make_plan(int64_t n, int64_t hq, int64_t kvh, int64_t seq_len, int64_t page_
   pl->pairs = kvh * pl->chunks;
   pl->groups = (pl->pairs + 7) / 8 * 8 * pl->row_blocks;
   const int64_t slots = pl->chunks > 1 ? kvh * pl->row_blocks * pl->chunks * 4 : 0;
-  pl->part_floats = slots * (kHD / 16) * 256;
-  pl->stats_floats = slots * 128;
+  pl->part_floats = slots * kPartHalves / 2;  // fp16 partials, counted in floats
+  pl->stats_floats = slots * kStatFloats;
   return TM_OK;
 }
 
@@ -538,9 +576,9 @@ extern "C" int tm_tree_attention(const void* q, int64_t q_stride, const void* k_
                      (hipStream_t)stream, p);
   TM_HIP_CHECK_LAUNCH();
   if (pl.chunks > 1) {
-    // kvh * row_blocks * 4 waves * 8 tiles * 64 lanes threads
+    // kvh * row_blocks * 4 waves * 16 groups * 64 lanes threads
     hipLaunchKernelGGL(tm_tree_attn_combine_kernel,
-                       dim3((unsigned)(kvh * pl.row_blocks * 4 * (kHD / 16) * 64 / kThreads)),
+                       dim3((unsigned)(kvh * pl.row_blocks * 4 * 16 * 64 / kThreads)),
                        dim3(kThreads), 0, (hipStream_t)stream, p);
     TM_HIP_CHECK_LAUNCH();
   }
