@@ -35,15 +35,19 @@ namespace {
 
 constexpr int PBM = 128;                 // rows per M-tile
 constexpr int PBN = 256;                 // weight rows per workgroup
-constexpr int PBK = 64;                  // K per pipeline step
+constexpr int PBK = 64;                  // K per pipeline step (K = 32 with two workgroups per CU measured 8 % slower)
 constexpr int NT = 512;                  // threads per workgroup (8 waves)
-constexpr int PROW = PBK * 2;            // LDS row, bytes (8 swizzled 16-byte chunks)
-constexpr int ABYTES = PBM * PROW;       // A tile of one step (16 KB)
-constexpr int BBYTES = PBN * PROW;       // B tile of one step (32 KB)
-constexpr int STAGE = ABYTES + BBYTES;   // 48 KB; three stages = 144 KB
-constexpr int ALD = ABYTES / (NT * 16);  // 16-byte loads per thread per step: A (2)
-constexpr int BLD = BBYTES / (NT * 16);  //                                   B (4)
-constexpr int LDS_PER_STEP = ALD + BLD;  // (6)
+constexpr int PROW = PBK * 2;            // LDS row, bytes (PROW / 16 swizzled chunks)
+constexpr int CPR = PROW / 16;           // 16-byte chunks per row
+constexpr int RPB = 256 / PROW;          // rows per 256 B (one pass over the 64 banks)
+constexpr int RPK = 1024 / PROW;         // rows per 1 KB load block
+constexpr int ABYTES = PBM * PROW;       // A tile of one step
+constexpr int BBYTES = PBN * PROW;       // B tile of one step
+constexpr int STAGE = ABYTES + BBYTES;   // three stages in LDS
+constexpr int ALD = ABYTES / (NT * 16);  // 16-byte loads per thread per step: A
+constexpr int BLD = BBYTES / (NT * 16);  //                                   B
+constexpr int LDS_PER_STEP = ALD + BLD;
+static_assert(ALD >= 1 && BLD >= 1 && CPR >= 4, "tile shape");
 constexpr uint32_t kOOR = 0x80000000u;   // out-of-range buffer offset: loads 0
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -67,8 +71,12 @@ __device__ __forceinline__ int acc_row(int v, int lane) {
   return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
 }
 
-// Byte offset in a swizzled tile of logical chunk c (16 B) of row r.
-__device__ __forceinline__ int swz(int r, int c) { return r * PROW + ((c ^ ((r >> 1) & 7)) << 4); }
+// Byte offset in a swizzled tile of logical chunk c (16 B) of row r: chunk c
+// is stored at c ^ ((r / RPB) % CPR), so 16 consecutive rows read at one
+// logical chunk cover 16 distinct 4-bank groups.
+__device__ __forceinline__ int swz(int r, int c) {
+  return r * PROW + ((c ^ ((r / RPB) & (CPR - 1))) << 4);
+}
 
 constexpr int SB = 8;  // super-block edge, in jobs
 
@@ -113,9 +121,9 @@ __device__ __forceinline__ bool find_mtile(const int32_t* __restrict__ offsets,
 }
 
 // Global -> LDS: load i of a thread moves one 16-byte chunk.  Load i of wave
-// w fills the 1 KB block 8 i + w of its tile (rows 8 (8 i + w) .. +7); lane l
-// writes byte 16 l of the block, i.e. row 8 (8 i + w) + l / 8 at stored chunk
-// l % 8, so it fetches the logical chunk (l % 8) ^ ((row >> 1) & 7).
+// w fills the 1 KB block 8 i + w of its tile (RPK rows); lane l writes byte
+// 16 l of the block, i.e. row RPK (8 i + w) + l / CPR at stored chunk
+// l % CPR, so it fetches the logical chunk that the swizzle stores there.
 struct DmaLoad {
   __amdgpu_buffer_rsrc_t ra, rb[BLD];
   uint32_t aoff[ALD];  // byte offset of the chunk at k = 0, or kOOR
@@ -124,10 +132,10 @@ struct DmaLoad {
 
 // Row of load i for this thread, and the logical chunk it fetches.
 __device__ __forceinline__ int dma_row(int i) {
-  return 8 * (8 * i + (threadIdx.x >> 6)) + ((threadIdx.x & 63) >> 3);
+  return RPK * (8 * i + (threadIdx.x >> 6)) + ((threadIdx.x & 63) / CPR);
 }
 __device__ __forceinline__ int dma_chunk(int row) {
-  return (threadIdx.x & 7) ^ ((row >> 1) & 7);
+  return (threadIdx.x & (CPR - 1)) ^ ((row / RPB) & (CPR - 1));
 }
 
 // Step `kstep` (K bytes 128 kstep ..) of both tiles into `st`; past the end
@@ -261,6 +269,7 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   for (int i = 0; i < BLD; ++i) {
     const int r = dma_row(i);  // loads 0, 1: B rows 0..127 (w1); 2, 3: 128..255 (w3, same n)
     d.rb[i] = i < BLD / 2 ? r1 : r3;
+    static_assert(BLD % 2 == 0, "w1 and w3 loads split evenly");
     d.boff[i] = (uint32_t)(n0 + (r & (PBN / 2 - 1))) * (uint32_t)H * 2u + (uint32_t)dma_chunk(r) * 16u;
   }
   f32x16_t acc[2][2];
