@@ -318,6 +318,43 @@ def secondary(m, inp2, args) -> dict:
                                         "us_device": round(dev_ms * 1e3, 2),
                                         "gbs_device": round(b / (dev_ms * 1e-3) / 1e9, 1),
                                         "accepted": num, "bytes_alg": b}
+    # sampling mode (temperature 1) and the repetition penalty at the same shape:
+    # device time of one C-ABI call each, inputs resident
+    g = torch.Generator().manual_seed(5)
+    q = torch.softmax(torch.randn(n, v, generator=g), -1).cuda()
+    uni = torch.rand(n, generator=g).cuda()
+    bu = torch.rand(1, generator=g).cuda()
+    resid = torch.empty(v, dtype=torch.float32, device=dev)
+
+    def sample_step():
+        _capi.call("tm_op4_sample_walk", logits.data_ptr(), _capi.TM_DTYPE_BF16, n, v,
+                   logits.stride(0), q.data_ptr(), q.stride(0), tokens.data_ptr(), csr.data_ptr(),
+                   csr.data_ptr() + 4 * n, csr.data_ptr() + 8 * n, uni.data_ptr(), bu.data_ptr(),
+                   1.0, resid.data_ptr(), slots.data_ptr(), toks.data_ptr(), result.data_ptr(),
+                   stream)
+
+    for _ in range(3):
+        sample_step()
+    sample_ms = events_time_ms(sample_step, max(reps, 50))
+    nodes_visited = int(result[1]) + 1
+    pen_logits = logits.clone()
+    prev = torch.randint(0, v, (512,), generator=g).cuda()
+    size = op4_commit._penalty_table_size(prev.numel())
+    table_ws = torch.empty(2 * size, dtype=torch.int32, device=dev)
+
+    def penalty_step():
+        _capi.call("tm_op4_rep_penalty", pen_logits.data_ptr(), _capi.TM_DTYPE_BF16, n, v,
+                   pen_logits.stride(0), prev.data_ptr(), prev.numel(), 1.1,
+                   table_ws.data_ptr(), size, stream)
+
+    for _ in range(3):
+        penalty_step()
+    pen_ms = events_time_ms(penalty_step, max(reps, 50))
+    out["config4_op4_sampling"] = {
+        "us_sample_walk": round(sample_ms * 1e3, 2), "nodes_visited": nodes_visited,
+        # per visited node: the row's softmax (3 logit passes) and the residual
+        # written once; per rejected child: q row read, residual read/written
+        "us_rep_penalty_512_prev_tokens": round(pen_ms * 1e3, 2)}
     out["config4_tree_attention"] = tree_attention_secondary(reps)
     return out
 
