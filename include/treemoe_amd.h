@@ -218,8 +218,9 @@ int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
  * of the num_prev tokens in order, x = x > 0 ? x / penalty : x * penalty, so a
  * token listed k times is penalised k times (bf16 rows are rounded after each
  * application, as the reference stores them).  Tokens outside [0, V) are
- * skipped.  `table`: 2 * table_size int32 of device memory, table_size a power
- * of two >= 2 * num_prev; no initial contents required.
+ * skipped.  `table`: 2 * table_size int32 of device memory, 16-byte aligned,
+ * table_size a power of two >= max(4, 2 * num_prev); no initial contents
+ * required.
  */
 int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V, int64_t row_stride,
                        const int64_t* prev_tokens, int64_t num_prev, float penalty,
@@ -238,8 +239,8 @@ int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V, int64_t ro
  * leaf) the bonus token is the smallest j with residual[0] + .. + residual[j] >
  * bonus_u[0] * sum (inverse CDF; the reference calls torch.multinomial).
  * draft_probs: [N, V] fp32, row stride q_stride.  uniforms [N], bonus_u [1]
- * fp32 on the device.  residual: V fp32 of device memory.  Outputs as
- * tm_op4_argmax_walk.
+ * fp32 on the device.  residual: V fp32 of device memory (the final residual
+ * on return).  V <= 2^25.  Outputs as tm_op4_argmax_walk.
  */
 int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int64_t V, int64_t row_stride,
                        const float* draft_probs, int64_t q_stride, const int64_t* tokens,

@@ -120,6 +120,10 @@ def test_tree_attention_plan():
     (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 1.5, 0, 4, 0), 1001),      # table < 2n
     (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 0.0, 0, 16, 0), 1003),     # penalty
     (("tm_op4_rep_penalty", 0, 5, 4, 10, 10, 0, 4, 1.5, 0, 16, 0), 1003),     # dtype
+    (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 1, 1.5, 0, 2, 0), 1001),      # table < 4
+    (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 1.5, 8, 16, 0), 1002),     # table align
+    (("tm_op4_sample_walk", 0, 0, 4, (1 << 25) + 1, 1 << 26, 0, 1 << 26, 0, 0, 0, 0, 0, 0, 1.0,
+      0, 0, 0, 0, 0), 1001),                                                    # V > 2^25
     (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 10, 0, 0, 0, 0, 0, 0, 0.0, 0, 0, 0, 0, 0),
      1003),                                                                     # temperature
     (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 9, 0, 0, 0, 0, 0, 0, 1.0, 0, 0, 0, 0, 0),

@@ -320,12 +320,17 @@ def _sampling_case(seed, n, v, follow):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("seed,n,v,temperature", [
     (1, 16, 64, 1.0), (2, 64, 32000, 0.7), (3, 33, 1000, 1.5), (4, 64, 32001, 1.0),
-    (5, 8, 5, 0.3), (6, 64, 4096, 2.0)])
+    (5, 8, 5, 0.3), (6, 64, 4096, 2.0), (7, 12, 32768, 1.0), (8, 12, 32769, 0.9),
+    (9, 16, 100000, 1.0), (10, 6, 9000, 1.2), (11, 2100, 300, 1.0), (12, 2100, 40000, 0.8)])
 def test_sampling_matches_oracle(dtype, seed, n, v, temperature):
     """Accept path, next root and bonus bit-exact against the oracle with the
     same uniforms; the final residual within rtol 1e-4 / atol 1e-6 (fp32
     softmax and residual updates with a different exp and summation order).
-    bf16 logits: the oracle gets them widened to fp32, as the kernel reads them."""
+    bf16 logits: the oracle gets them widened to fp32, as the kernel reads them.
+    V up to 32768 runs the register-resident walk (8, 16 or 32 entries per
+    thread), larger V the tiled walk over a global residual (32769: a one-entry
+    second tile; 100000: four tiles).  Trees of more than 2048 nodes are walked
+    from global memory instead of LDS (n = 2100, both walks)."""
     _say(f"sampling seed={seed} n={n} v={v} T={temperature} {dtype}")
     for rep in range(4):
         g, children, tokens, logits, q = _sampling_case(seed * 10 + rep, n, v, 0.8)

@@ -247,31 +247,46 @@ tm_kv_commit_kernel(uint8_t* __restrict__ k, uint8_t* __restrict__ v, int64_t ro
 // (op4_commit.py:53-57): for each prev token t (in order),
 //   x[row, t] = x > 0 ? x / penalty : x * penalty,
 // so a token listed k times is penalised k times.  The same function is
-// applied each time, so only the count of each token matters: one workgroup
-// counts the distinct tokens in an open-addressing table (global workspace,
-// 2 * S int32 for S = table size, a power of two >= 2 * num_prev), then
-// applies each token's count to every row.  Tokens outside [0, V) are skipped.
+// applied each time, so only the count of each token matters.  One workgroup
+// counts the distinct tokens in an open-addressing table of S slots (S a
+// power of two >= 2 * num_prev; keys then counts, 2 * S int32 of global
+// workspace), then a grid over (row, block of slots) applies each counted
+// token's penalty.  Tokens outside [0, V) are skipped.
 constexpr int kPenThreads = 1024;
+constexpr int kPenLdsSlots = 8192;     // tables up to this size are built in LDS
+constexpr int kApplyThreads = 256;
+constexpr int kApplySlots = 4;         // table slots per thread (one 16-byte load)
+constexpr int kApplyBlock = kApplyThreads * kApplySlots;
 
-template <int kDtype>
+__device__ __forceinline__ uint32_t pen_hash(int64_t t, int S) {
+  return ((uint32_t)t * 2654435761u) & (uint32_t)(S - 1);
+}
+
+// kLds: the table lives in LDS and is copied out at the end.  Otherwise every
+// access is an agent-scope atomic on the global table, coherent at L2 whatever
+// the L1 holds.  Either way the barriers order init, insert and copy-out.
+template <bool kLds>
 __global__ void __launch_bounds__(kPenThreads)
-tm_rep_penalty_kernel(void* __restrict__ logits, int N, int V, int64_t row_stride,
-                      const int64_t* __restrict__ prev, int num_prev, float penalty,
-                      int32_t* __restrict__ table, int S) {
-  int32_t* keys = table;
-  int32_t* counts = table + S;
+tm_rep_count_kernel(const int64_t* __restrict__ prev, int num_prev, int V,
+                    int32_t* __restrict__ table, int S) {
+  __shared__ int32_t s_tab[kLds ? 2 * kPenLdsSlots : 1];
+  int32_t* keys = kLds ? s_tab : table;
+  int32_t* counts = kLds ? s_tab + S : table + S;
   const int tid = threadIdx.x;
-  // every table access is an agent-scope atomic, so the table is coherent at
-  // L2 whatever the L1 holds; the barriers order the three phases
   for (int i = tid; i < S; i += kPenThreads) {
-    __hip_atomic_store(&keys[i], -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&counts[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (kLds) {
+      keys[i] = -1;
+      counts[i] = 0;
+    } else {
+      __hip_atomic_store(&keys[i], -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&counts[i], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   for (int i = tid; i < num_prev; i += kPenThreads) {
     const int64_t t = prev[i];
     if (t < 0 || t >= V) continue;
-    uint32_t h = ((uint32_t)t * 2654435761u) & (uint32_t)(S - 1);
+    uint32_t h = pen_hash(t, S);
     for (int probe = 0; probe < S; ++probe) {
       const int prior = atomicCAS(&keys[h], -1, (int)t);
       if (prior == -1 || prior == (int)t) {
@@ -281,29 +296,49 @@ tm_rep_penalty_kernel(void* __restrict__ logits, int N, int V, int64_t row_strid
       h = (h + 1) & (uint32_t)(S - 1);
     }
   }
-  __syncthreads();
-  const int64_t pairs = (int64_t)S * N;
-  for (int64_t q = tid; q < pairs; q += kPenThreads) {
-    const int slot = (int)(q % S);
-    const int row = (int)(q / S);
-    const int k = __hip_atomic_load(&counts[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (k == 0) continue;
-    const int key = __hip_atomic_load(&keys[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t at = (int64_t)row * row_stride + key;
-    if (kDtype == TM_DTYPE_F32) {
-      float* x = reinterpret_cast<float*>(logits) + at;
-      float v = *x;
-      for (int r = 0; r < k; ++r) v = v > 0.0f ? v / penalty : v * penalty;
-      *x = v;
-    } else {
-      // the reference stores (rounds to bf16) after every application
-      uint16_t* x = reinterpret_cast<uint16_t*>(logits) + at;
-      uint16_t b = *x;
-      for (int r = 0; r < k; ++r) {
-        const float v = tm_bf16_to_f32(b);
-        b = tm_f32_to_bf16(v > 0.0f ? v / penalty : v * penalty);
+  if (kLds) {
+    __syncthreads();
+    for (int i = tid; i < S; i += kPenThreads) {
+      table[i] = keys[i];
+      table[S + i] = counts[i];
+    }
+  }
+}
+
+// grid (N, slot blocks): thread reads kApplySlots (key, count) pairs with one
+// 16-byte load each and applies every counted token to its row.  Distinct
+// slots hold distinct tokens, so no two threads touch one logit.
+template <int kDtype>
+__global__ void __launch_bounds__(kApplyThreads)
+tm_rep_apply_kernel(void* __restrict__ logits, int64_t row_stride,
+                    const int32_t* __restrict__ table, int S, float penalty) {
+  const int64_t row = blockIdx.x;
+  for (int base = (blockIdx.y * kApplyThreads + threadIdx.x) * kApplySlots; base < S;
+       base += gridDim.y * kApplyBlock) {
+    const int4 k4 = *reinterpret_cast<const int4*>(table + base);
+    const int4 c4 = *reinterpret_cast<const int4*>(table + S + base);
+    const int keys[4] = {k4.x, k4.y, k4.z, k4.w};
+    const int counts[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+    for (int j = 0; j < kApplySlots; ++j) {
+      const int k = counts[j];
+      if (k == 0) continue;
+      const int64_t at = row * row_stride + keys[j];
+      if (kDtype == TM_DTYPE_F32) {
+        float* x = reinterpret_cast<float*>(logits) + at;
+        float v = *x;
+        for (int r = 0; r < k; ++r) v = v > 0.0f ? v / penalty : v * penalty;
+        *x = v;
+      } else {
+        // the reference stores (rounds to bf16) after every application
+        uint16_t* x = reinterpret_cast<uint16_t*>(logits) + at;
+        uint16_t b = *x;
+        for (int r = 0; r < k; ++r) {
+          const float v = tm_bf16_to_f32(b);
+          b = tm_f32_to_bf16(v > 0.0f ? v / penalty : v * penalty);
+        }
+        *x = b;
       }
-      *x = b;
     }
   }
 }
@@ -321,13 +356,6 @@ tm_rep_penalty_kernel(void* __restrict__ logits, int N, int V, int64_t row_strid
 constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 
-struct SampShared {
-  float red[kSampWaves];
-  float bcast[2];
-  int flag;
-  int count;
-};
-
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
@@ -340,21 +368,14 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Workgroup sum (is_max = false) or max in a fixed order; every thread gets it.
-__device__ __forceinline__ float block_reduce(float v, bool is_max, SampShared& sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  v = is_max ? wave_max(v) : wave_sum(v);
-  if (lane == 0) sh.red[wave] = v;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float r = sh.red[0];
-    for (int w = 1; w < kSampWaves; ++w) r = is_max ? fmaxf(r, sh.red[w]) : r + sh.red[w];
-    sh.bcast[0] = r;
-  }
-  __syncthreads();
-  const float r = sh.bcast[0];
-  __syncthreads();
-  return r;
+// x / d, correctly rounded, from rcp = 1 / d (itself correctly rounded):
+// Markstein's correction q + (x - q d) * rcp, whose residual x - q d one FMA
+// gives exactly.  Three VALU operations instead of the IEEE division sequence;
+// a non-finite quotient (a -inf logit) is returned as x * rcp.
+__device__ __forceinline__ float div_by(float x, float d, float rcp) {
+  const float q = x * rcp;
+  const float c = fmaf(fmaf(-q, d, x), rcp, q);
+  return __builtin_isfinite(q) ? c : q;
 }
 
 template <int kDtype>
@@ -363,72 +384,321 @@ __device__ __forceinline__ float logit_at(const void* logits, int64_t at) {
   return tm_bf16_to_f32(reinterpret_cast<const uint16_t*>(logits)[at]);
 }
 
-template <int kDtype>
+
+// ----------------------------------------------- sampling, in registers --
+// For V <= kSampThreads * R: thread t owns residual entries
+// [t * R, t * R + R) in registers, so a row pass issues every load of the
+// thread at once instead of one dependent load per loop trip, and the bonus
+// scan is a shuffle scan.  Entries at or past V hold 0 (-inf as logits).
+// Reductions are in a fixed order: the thread's entries in index order, then
+// a butterfly over the wave, then the 16 wave values in wave order.
+struct SampRegShared {
+  float red[2][kSampWaves];  // alternating buffers: one barrier per reduction
+  float wsum[kSampWaves];
+  int flag;
+  int pick;
+};
+
+// Trees up to kSampStage nodes are staged in LDS before the walk, together
+// with the one draft probability each child's accept test reads,
+// q[c][tokens[c]], gathered for all nodes at once; the walk's per-child reads
+// are then LDS reads.  Larger trees are read from global memory.
+constexpr int kSampStage = 2048;
+
+struct SampTree {
+  int tok[kSampStage];          // tokens[c], -1 outside [0, V)
+  int child_start[kSampStage];
+  int child_count[kSampStage];
+  int child_list[kSampStage];
+  float u[kSampStage];          // uniforms[c]
+  float qtok[kSampStage];       // q[c][tokens[c]], 0 outside [0, V)
+};
+
+__device__ __forceinline__ void stage_tree(SampTree& s, int N, int V,
+                                           const int64_t* __restrict__ tokens,
+                                           const int32_t* __restrict__ child_start,
+                                           const int32_t* __restrict__ child_count,
+                                           const int32_t* __restrict__ child_list,
+                                           const float* __restrict__ uniforms,
+                                           const float* __restrict__ q, int64_t q_stride) {
+  const int nlist = N > 1 ? N - 1 : 1;
+  for (int i = threadIdx.x; i < N; i += kSampThreads) {
+    const int64_t t = tokens[i];
+    const bool in = t >= 0 && t < V;
+    s.tok[i] = in ? (int)t : -1;
+    s.child_start[i] = child_start[i];
+    s.child_count[i] = child_count[i];
+    s.u[i] = uniforms[i];
+    s.qtok[i] = in ? q[(int64_t)i * q_stride + t] : 0.0f;
+  }
+  for (int i = threadIdx.x; i < nlist; i += kSampThreads) s.child_list[i] = child_list[i];
+  __syncthreads();
+}
+
+// Child list entry `at` (staged or from global memory): the child's slot c
+// and its token (-1 outside [0, V)).
+__device__ __forceinline__ int2 sample_child(bool staged, const SampTree& s, int at, int V,
+                                             const int64_t* __restrict__ tokens,
+                                             const int32_t* __restrict__ child_list) {
+  if (staged) {
+    const int c = s.child_list[at];
+    return make_int2(c, s.tok[c]);
+  }
+  const int c = child_list[at];
+  const int64_t t = tokens[c];
+  return make_int2(c, (t >= 0 && t < V) ? (int)t : -1);
+}
+
+// The accept test of child c with in-vocabulary token tok, given the
+// residual's entry rv: u_c < min(rv / max(q_c[tok], 1e-20), 1).
+__device__ __forceinline__ int sample_accept(bool staged, const SampTree& s, int c, int tok,
+                                             float rv, const float* __restrict__ uniforms,
+                                             const float* __restrict__ q, int64_t q_stride) {
+  const float u = staged ? s.u[c] : uniforms[c];
+  const float qt = staged ? s.qtok[c] : q[(int64_t)c * q_stride + tok];
+  const float ratio = fminf(rv / fmaxf(qt, 1e-20f), 1.0f);
+  return u < ratio ? 1 : 0;
+}
+
+__device__ __forceinline__ float block_reduce_fast(float v, bool is_max, SampRegShared& sh,
+                                                   int& phase) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = is_max ? wave_max(v) : wave_sum(v);
+  float* buf = sh.red[phase];
+  phase ^= 1;
+  if (lane == 0) buf[wave] = v;
+  __syncthreads();
+  float r = buf[0];
+#pragma unroll
+  for (int w = 1; w < kSampWaves; ++w) r = is_max ? fmaxf(r, buf[w]) : r + buf[w];
+  return r;
+}
+
+// x[i] = element lo + i of a row of `kDtype` (fill beyond V); 16-byte loads
+// when the row is aligned and the thread's range lies inside [0, V).
+template <int kDtype, int R>
+__device__ __forceinline__ void load_range(const void* row, int lo, int V, bool vec, float fill,
+                                           float (&x)[R]) {
+  if (vec && lo + R <= V) {
+    if (kDtype == TM_DTYPE_F32) {
+      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(row) + lo);
+#pragma unroll
+      for (int j = 0; j < R / 4; ++j) {
+        const float4 f = p[j];
+        x[4 * j] = f.x;
+        x[4 * j + 1] = f.y;
+        x[4 * j + 2] = f.z;
+        x[4 * j + 3] = f.w;
+      }
+    } else {
+      const uint4* p = reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(row) + lo);
+#pragma unroll
+      for (int j = 0; j < R / 8; ++j) {
+        const uint4 u = p[j];
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          x[8 * j + 2 * k] = __uint_as_float(w[k] << 16);
+          x[8 * j + 2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      x[i] = (lo + i < V) ? logit_at<kDtype>(row, lo + i) : fill;
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void store_range(float* dst, int lo, int V, bool vec,
+                                            const float (&x)[R]) {
+  if (vec && lo + R <= V) {
+    float4* p = reinterpret_cast<float4*>(dst + lo);
+#pragma unroll
+    for (int j = 0; j < R / 4; ++j)
+      p[j] = make_float4(x[4 * j], x[4 * j + 1], x[4 * j + 2], x[4 * j + 3]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      if (lo + i < V) dst[lo + i] = x[i];
+  }
+}
+
+// Inclusive prefix sums of the threads' chunk sums in thread order, starting
+// from `base`: returns this thread's, sets `exc` to the previous thread's
+// (`base` for thread 0; the very value that thread returns) and `total` to
+// thread kSampThreads - 1's.  Also resets sh.pick for block_pick.
+__device__ __forceinline__ float block_scan(float csum, float base, float& exc, float& total,
+                                            SampRegShared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float inc = csum;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float t = __shfl_up(inc, off);
+    if (lane >= off) inc = inc + t;
+  }
+  if (lane == 63) sh.wsum[wave] = inc;
+  if (threadIdx.x == 0) sh.pick = INT_MAX;
+  __syncthreads();
+  float wbase = base, run = base;
+#pragma unroll
+  for (int w = 0; w < kSampWaves; ++w) {
+    if (w == wave) wbase = run;
+    run = run + sh.wsum[w];
+  }
+  total = run;
+  inc = wbase + inc;
+  exc = __shfl_up(inc, 1);
+  if (lane == 0) exc = wbase;
+  return inc;
+}
+
+// Inverse CDF within one block scan: the first thread whose inclusive sum
+// passes `target` walks its chunk x[0..R) (entries lo..) from `exc` and picks
+// the first entry whose running sum passes it (its last nonzero entry when
+// rounding leaves the target at the chunk's end).  Returns the pick to every
+// thread, -1 when no thread passes.
+template <int R>
+__device__ __forceinline__ int block_pick(const float (&x)[R], int lo, float inc, float exc,
+                                          float target, SampRegShared& sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t pass = __ballot(inc > target);
+  if (lane == 0 && pass != 0) atomicMin(&sh.pick, wave * 64 + __builtin_ctzll(pass));
+  __syncthreads();
+  if ((int)threadIdx.x == sh.pick) {
+    int pick = -1, last = -1;
+    float run = exc;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      run = run + x[i];
+      if (pick < 0 && run > target) pick = lo + i;
+      if (x[i] > 0.0f) last = lo + i;
+    }
+    sh.flag = pick >= 0 ? pick : last;
+  }
+  if (threadIdx.x == 0 && sh.pick == INT_MAX) sh.flag = -1;
+  __syncthreads();
+  return sh.flag;
+}
+
+// Workgroup max of an int (one reduction slot, as block_reduce_fast).
+__device__ __forceinline__ int block_max_int(int v, SampRegShared& sh, int& phase) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off));
+  float* buf = sh.red[phase];
+  phase ^= 1;
+  if (lane == 0) buf[wave] = __int_as_float(v);
+  __syncthreads();
+  int r = __float_as_int(buf[0]);
+#pragma unroll
+  for (int w = 1; w < kSampWaves; ++w) r = max(r, __float_as_int(buf[w]));
+  return r;
+}
+
+template <int R>
+__device__ __forceinline__ int last_nonzero(const float (&x)[R], int lo, int last) {
+#pragma unroll
+  for (int i = 0; i < R; ++i)
+    if (x[i] > 0.0f) last = lo + i;
+  return last;
+}
+
+template <int kDtype, int R>
 __global__ void __launch_bounds__(kSampThreads)
-tm_sample_walk_kernel(const void* __restrict__ logits, int N, int V, int64_t row_stride,
-                      const float* __restrict__ q, int64_t q_stride,
-                      const int64_t* __restrict__ tokens, const int32_t* __restrict__ child_start,
-                      const int32_t* __restrict__ child_count,
-                      const int32_t* __restrict__ child_list, const float* __restrict__ uniforms,
-                      const float* __restrict__ bonus_u, float temperature,
-                      float* __restrict__ res, int64_t* __restrict__ accepted_slots,
-                      int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result) {
-  __shared__ SampShared sh;
+tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t row_stride,
+                          int vec_logits, const float* __restrict__ q, int64_t q_stride,
+                          int vec_q, const int64_t* __restrict__ tokens,
+                          const int32_t* __restrict__ child_start,
+                          const int32_t* __restrict__ child_count,
+                          const int32_t* __restrict__ child_list,
+                          const float* __restrict__ uniforms, const float* __restrict__ bonus_u,
+                          float temperature, float* __restrict__ res, int vec_res,
+                          int64_t* __restrict__ accepted_slots,
+                          int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result) {
+  __shared__ SampRegShared sh;
+  __shared__ SampTree tree;
   const int tid = threadIdx.x;
+  const int lo = tid * R;
+  const bool staged = N <= kSampStage;
+  if (staged)
+    stage_tree(tree, N, V, tokens, child_start, child_count, child_list, uniforms, q, q_stride);
+  int phase = 0;
+  const float rtemp = 1.0f / temperature;
   int node = 0;
   int count = 0;
+  float r[R];
   for (;;) {
-    // residual = softmax(logits[node] / temperature)
-    const int64_t base = (int64_t)node * row_stride;
+    // r = softmax(logits[node] / temperature)
+    const char* row = reinterpret_cast<const char*>(logits) +
+                      (int64_t)node * row_stride * (kDtype == TM_DTYPE_F32 ? 4 : 2);
+    load_range<kDtype, R>(row, lo, V, vec_logits != 0, -INFINITY, r);
     float m = -INFINITY;
-    for (int v = tid; v < V; v += kSampThreads)
-      m = fmaxf(m, logit_at<kDtype>(logits, base + v) / temperature);
-    m = block_reduce(m, true, sh);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      r[i] = div_by(r[i], temperature, rtemp);
+      m = fmaxf(m, r[i]);
+    }
+    m = block_reduce_fast(m, true, sh, phase);
     float s = 0.0f;
-    for (int v = tid; v < V; v += kSampThreads)
-      s = s + tm_expf_det(logit_at<kDtype>(logits, base + v) / temperature - m);
-    s = block_reduce(s, false, sh);
-    for (int v = tid; v < V; v += kSampThreads)
-      res[v] = tm_expf_det(logit_at<kDtype>(logits, base + v) / temperature - m) / s;
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+      r[i] = tm_expf_det(r[i] - m);
+      s = s + r[i];
+    }
+    // the normalisations multiply by a reciprocal (within an ulp of dividing)
+    const float rs = 1.0f / block_reduce_fast(s, false, sh, phase);
+#pragma unroll
+    for (int i = 0; i < R; ++i) r[i] = r[i] * rs;
 
-    const int st = child_start[node];
-    const int cnt = child_count[node];
-    int taken = -1;
+    const int st = staged ? tree.child_start[node] : child_start[node];
+    const int cnt = staged ? tree.child_count[node] : child_count[node];
+    int taken = -1, taken_tok = -1;
     for (int j = 0; j < cnt; ++j) {
-      const int c = child_list[st + j];
-      if (tid == 0) {
-        const int64_t tok = tokens[c];
+      const int2 ct = sample_child(staged, tree, st + j, V, tokens, child_list);
+      const int c = ct.x, tok = ct.y;
+      // the owner of entry tok decides; tid 0 answers for an out-of-vocabulary token
+      if (tok >= 0 ? tok / R == tid : tid == 0) {
         int ok = 0;
-        if (tok >= 0 && tok < V) {
-          float ratio = res[tok] / fmaxf(q[(int64_t)c * q_stride + tok], 1e-20f);
-          ratio = fminf(ratio, 1.0f);
-          ok = uniforms[c] < ratio ? 1 : 0;
+        if (tok >= 0) {
+          float rv = 0.0f;
+#pragma unroll
+          for (int i = 0; i < R; ++i) rv = (lo + i == tok) ? r[i] : rv;
+          ok = sample_accept(staged, tree, c, tok, rv, uniforms, q, q_stride);
         }
         sh.flag = ok;
       }
       __syncthreads();
-      const int ok = sh.flag;
-      __syncthreads();
-      if (ok) {
+      if (sh.flag) {
         taken = c;
+        taken_tok = tok;
         break;
       }
-      const float* qc = q + (int64_t)c * q_stride;
+      // rejected: r = max(r - q_c, 0) / sum (the reduction's barrier also
+      // orders this read of sh.flag before the next write); q_c is read in
+      // blocks of at most 16 entries, which bounds the registers live beside r
+      constexpr int kQB = R < 16 ? R : 16;
       float part = 0.0f;
-      for (int v = tid; v < V; v += kSampThreads) {
-        const float r = fmaxf(res[v] - qc[v], 0.0f);
-        res[v] = r;
-        part = part + r;
+#pragma unroll
+      for (int b = 0; b < R; b += kQB) {
+        float qc[kQB];
+        load_range<TM_DTYPE_F32, kQB>(q + (int64_t)c * q_stride, lo + b, V, vec_q != 0, 0.0f,
+                                      qc);
+#pragma unroll
+        for (int i = 0; i < kQB; ++i) {
+          r[b + i] = fmaxf(r[b + i] - qc[i], 0.0f);
+          part = part + r[b + i];
+        }
       }
-      const float tot = fmaxf(block_reduce(part, false, sh), 1e-20f);
-      for (int v = tid; v < V; v += kSampThreads) res[v] = res[v] / tot;
-      __syncthreads();
+      const float rtot = 1.0f / fmaxf(block_reduce_fast(part, false, sh, phase), 1e-20f);
+#pragma unroll
+      for (int i = 0; i < R; ++i) r[i] = r[i] * rtot;
     }
     if (taken >= 0 && count < N) {
       if (tid == 0) {
         accepted_slots[count] = taken;
-        accepted_tokens[count] = tokens[taken];
+        accepted_tokens[count] = taken_tok;
       }
       ++count;
       node = taken;
@@ -437,60 +707,246 @@ tm_sample_walk_kernel(const void* __restrict__ logits, int N, int V, int64_t row
     break;
   }
 
-  // bonus: smallest j with res[0] + .. + res[j] > bonus_u * total, chunked
-  // prefix sums (thread t owns a contiguous chunk; chunk sums scanned in
-  // thread order)
-  const int cs = (V + kSampThreads - 1) / kSampThreads;
-  const int lo = min(V, tid * cs), hi = min(V, lo + cs);
+  // bonus: smallest j with r[0] + .. + r[j] > bonus_u * total
   float csum = 0.0f;
-  for (int v = lo; v < hi; ++v) csum = csum + res[v];
-  // exclusive scan of chunk sums over the workgroup, in thread order
-  __shared__ float s_chunk[kSampThreads];
-  s_chunk[tid] = csum;
-  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < R; ++i) csum = csum + r[i];
+  float exc, total;
+  const float inc = block_scan(csum, 0.0f, exc, total, sh);
+  int bonus = block_pick<R>(r, lo, inc, exc, bonus_u[0] * total, sh);
+  if (bonus < 0)  // target at or past the total: the last nonzero entry
+    bonus = max(block_max_int(last_nonzero<R>(r, lo, -1), sh, phase), 0);
   if (tid == 0) {
-    float run = 0.0f;
-    for (int t = 0; t < kSampThreads; ++t) {
-      const float c = s_chunk[t];
-      s_chunk[t] = run;
-      run = run + c;
-    }
-    sh.bcast[1] = run;
-    sh.flag = INT_MAX;
-  }
-  __syncthreads();
-  const float target = bonus_u[0] * sh.bcast[1];
-  float run = s_chunk[tid];
-  // exactly one chunk satisfies this (the boundaries are the same rounded sums)
-  if (run <= target && target < run + csum) {
-    int pick = hi - 1;
-    for (int v = lo; v < hi; ++v) {
-      run = run + res[v];
-      if (run > target) {
-        pick = v;
-        break;
-      }
-    }
-    atomicMin(&sh.flag, pick);
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int bonus = sh.flag;
-    if (bonus == INT_MAX) {  // target at or past the total: last nonzero entry
-      bonus = 0;
-      for (int v = V - 1; v >= 0; --v)
-        if (res[v] > 0.0f) { bonus = v; break; }
-    }
     result[0] = bonus;
     result[1] = count;
     result[2] = node;
-    sh.count = count;
   }
-  __syncthreads();
-  for (int i = sh.count + tid; i < N; i += kSampThreads) {
+  store_range<R>(res, lo, V, vec_res != 0, r);
+  for (int i = count + tid; i < N; i += kSampThreads) {
     accepted_slots[i] = -1;
     accepted_tokens[i] = -1;
   }
+}
+
+// ------------------------------------------------- sampling, in tiles --
+// For V > kSampRegMax: the residual lives in `res` and every pass walks the
+// row in tiles of kSampTile entries; thread t owns entries
+// [tile * kSampTile + t * kSampTR, + kSampTR) of every tile, so it issues a
+// tile's loads at once and only ever reads back residual entries it wrote
+// itself.  Sums accumulate over the thread's entries tile by tile, then as in
+// the register kernel.  The bonus scan finds the tile whose running total
+// (tile totals in tile order) passes the target, then scans that tile.
+constexpr int kSampTR = 32;
+constexpr int kSampTile = kSampThreads * kSampTR;
+constexpr int kSampRegMax = kSampTile;          // V up to this: the register kernel
+constexpr int kSampMaxTiles = 1024;             // tile totals kept in LDS
+constexpr int64_t kSampMaxV = (int64_t)kSampMaxTiles * kSampTile;
+
+template <int kDtype>
+__global__ void __launch_bounds__(kSampThreads)
+tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64_t row_stride,
+                            int vec_logits, const float* __restrict__ q, int64_t q_stride,
+                            int vec_q, const int64_t* __restrict__ tokens,
+                            const int32_t* __restrict__ child_start,
+                            const int32_t* __restrict__ child_count,
+                            const int32_t* __restrict__ child_list,
+                            const float* __restrict__ uniforms, const float* __restrict__ bonus_u,
+                            float temperature, float* __restrict__ res, int vec_res,
+                            int64_t* __restrict__ accepted_slots,
+                            int64_t* __restrict__ accepted_tokens,
+                            int64_t* __restrict__ result) {
+  __shared__ SampRegShared sh;
+  __shared__ SampTree tree;
+  __shared__ float s_tile[kSampMaxTiles];
+  const int tid = threadIdx.x;
+  const int tiles = (V + kSampTile - 1) / kSampTile;
+  const bool vl = vec_logits != 0, vq = vec_q != 0, vr = vec_res != 0;
+  const bool staged = N <= kSampStage;
+  if (staged)
+    stage_tree(tree, N, V, tokens, child_start, child_count, child_list, uniforms, q, q_stride);
+  const float rtemp = 1.0f / temperature;
+  int phase = 0;
+  int node = 0;
+  int count = 0;
+  for (;;) {
+    // res = softmax(logits[node] / temperature): max, sum, then the entries
+    const char* row = reinterpret_cast<const char*>(logits) +
+                      (int64_t)node * row_stride * (kDtype == TM_DTYPE_F32 ? 4 : 2);
+    float m = -INFINITY;
+    for (int tl = 0; tl < tiles; ++tl) {
+      float x[kSampTR];
+      load_range<kDtype, kSampTR>(row, tl * kSampTile + tid * kSampTR, V, vl, -INFINITY, x);
+#pragma unroll
+      for (int i = 0; i < kSampTR; ++i) m = fmaxf(m, div_by(x[i], temperature, rtemp));
+    }
+    m = block_reduce_fast(m, true, sh, phase);
+    // the exponentials go to res, then one pass scales them by 1 / sum
+    float s = 0.0f;
+    for (int tl = 0; tl < tiles; ++tl) {
+      const int lo = tl * kSampTile + tid * kSampTR;
+      float x[kSampTR];
+      load_range<kDtype, kSampTR>(row, lo, V, vl, -INFINITY, x);
+#pragma unroll
+      for (int i = 0; i < kSampTR; ++i) {
+        x[i] = tm_expf_det(div_by(x[i], temperature, rtemp) - m);
+        s = s + x[i];
+      }
+      store_range<kSampTR>(res, lo, V, vr, x);
+    }
+    const float rs = 1.0f / block_reduce_fast(s, false, sh, phase);
+    for (int tl = 0; tl < tiles; ++tl) {
+      const int lo = tl * kSampTile + tid * kSampTR;
+      float x[kSampTR];
+      load_range<TM_DTYPE_F32, kSampTR>(res, lo, V, vr, 0.0f, x);
+#pragma unroll
+      for (int i = 0; i < kSampTR; ++i) x[i] = x[i] * rs;
+      store_range<kSampTR>(res, lo, V, vr, x);
+    }
+
+    const int st = staged ? tree.child_start[node] : child_start[node];
+    const int cnt = staged ? tree.child_count[node] : child_count[node];
+    int taken = -1, taken_tok = -1;
+    for (int j = 0; j < cnt; ++j) {
+      const int2 ct = sample_child(staged, tree, st + j, V, tokens, child_list);
+      const int c = ct.x, tok = ct.y;
+      // the thread that wrote res[tok] decides; tid 0 for an out-of-vocabulary token
+      if (tok >= 0 ? (tok % kSampTile) / kSampTR == tid : tid == 0) {
+        int ok = 0;
+        if (tok >= 0) ok = sample_accept(staged, tree, c, tok, res[tok], uniforms, q, q_stride);
+        sh.flag = ok;
+      }
+      __syncthreads();
+      if (sh.flag) {
+        taken = c;
+        taken_tok = tok;
+        break;
+      }
+      const float* qrow = q + (int64_t)c * q_stride;
+      float part = 0.0f;
+      for (int tl = 0; tl < tiles; ++tl) {
+        const int lo = tl * kSampTile + tid * kSampTR;
+        float x[kSampTR], qc[kSampTR];
+        load_range<TM_DTYPE_F32, kSampTR>(res, lo, V, vr, 0.0f, x);
+        load_range<TM_DTYPE_F32, kSampTR>(qrow, lo, V, vq, 0.0f, qc);
+#pragma unroll
+        for (int i = 0; i < kSampTR; ++i) {
+          x[i] = fmaxf(x[i] - qc[i], 0.0f);
+          part = part + x[i];
+        }
+        store_range<kSampTR>(res, lo, V, vr, x);
+      }
+      const float rtot = 1.0f / fmaxf(block_reduce_fast(part, false, sh, phase), 1e-20f);
+      for (int tl = 0; tl < tiles; ++tl) {
+        const int lo = tl * kSampTile + tid * kSampTR;
+        float x[kSampTR];
+        load_range<TM_DTYPE_F32, kSampTR>(res, lo, V, vr, 0.0f, x);
+#pragma unroll
+        for (int i = 0; i < kSampTR; ++i) x[i] = x[i] * rtot;
+        store_range<kSampTR>(res, lo, V, vr, x);
+      }
+    }
+    if (taken >= 0 && count < N) {
+      if (tid == 0) {
+        accepted_slots[count] = taken;
+        accepted_tokens[count] = taken_tok;
+      }
+      ++count;
+      node = taken;
+      continue;
+    }
+    break;
+  }
+
+  // bonus: tile totals in tile order, then the scan of the tile that passes
+  float total = 0.0f;
+  for (int tl = 0; tl < tiles; ++tl) {
+    float x[kSampTR];
+    load_range<TM_DTYPE_F32, kSampTR>(res, tl * kSampTile + tid * kSampTR, V, vr, 0.0f, x);
+    float csum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSampTR; ++i) csum = csum + x[i];
+    const float t = block_reduce_fast(csum, false, sh, phase);
+    if (tid == 0) s_tile[tl] = t;
+    total = total + t;
+  }
+  __syncthreads();
+  const float target = bonus_u[0] * total;
+  float base = 0.0f;
+  int ct = -1;
+  for (int tl = 0; tl < tiles; ++tl) {
+    const float next = base + s_tile[tl];
+    if (next > target) {
+      ct = tl;
+      break;
+    }
+    base = next;
+  }
+  int bonus = -1;
+  if (ct >= 0) {
+    const int lo = ct * kSampTile + tid * kSampTR;
+    float x[kSampTR];
+    load_range<TM_DTYPE_F32, kSampTR>(res, lo, V, vr, 0.0f, x);
+    float csum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSampTR; ++i) csum = csum + x[i];
+    float exc, tile_end;
+    const float inc = block_scan(csum, base, exc, tile_end, sh);
+    bonus = block_pick<kSampTR>(x, lo, inc, exc, target, sh);
+    // rounding left the target past this tile's scan: its last nonzero entry
+    if (bonus < 0) bonus = block_max_int(last_nonzero<kSampTR>(x, lo, -1), sh, phase);
+  }
+  if (bonus < 0) {
+    // target at or past the total: the last nonzero entry
+    int last = -1;
+    for (int tl = 0; tl < tiles; ++tl) {
+      const int lo = tl * kSampTile + tid * kSampTR;
+      float x[kSampTR];
+      load_range<TM_DTYPE_F32, kSampTR>(res, lo, V, vr, 0.0f, x);
+      last = last_nonzero<kSampTR>(x, lo, last);
+    }
+    bonus = max(block_max_int(last, sh, phase), 0);
+  }
+  if (tid == 0) {
+    result[0] = bonus;
+    result[1] = count;
+    result[2] = node;
+  }
+  for (int i = count + tid; i < N; i += kSampThreads) {
+    accepted_slots[i] = -1;
+    accepted_tokens[i] = -1;
+  }
+}
+
+template <int kDtype>
+void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, const float* q,
+                        int64_t q_stride, const int64_t* tokens, const int32_t* child_start,
+                        const int32_t* child_count, const int32_t* child_list,
+                        const float* uniforms, const float* bonus_u, float temperature,
+                        float* res, int64_t* accepted_slots, int64_t* accepted_tokens,
+                        int64_t* result, hipStream_t stream) {
+  const int64_t elem = kDtype == TM_DTYPE_F32 ? 4 : 2;
+  const int vl = ((uintptr_t)logits % 16 == 0 && (row_stride * elem) % 16 == 0) ? 1 : 0;
+  const int vq = ((uintptr_t)q % 16 == 0 && q_stride % 4 == 0) ? 1 : 0;
+  const int vr = ((uintptr_t)res % 16 == 0) ? 1 : 0;
+#define TM_SAMPLE_REG(R)                                                                       \
+  hipLaunchKernelGGL((tm_sample_walk_reg_kernel<kDtype, R>), dim3(1), dim3(kSampThreads), 0,   \
+                     stream, logits, N, V, row_stride, vl, q, q_stride, vq, tokens,           \
+                     child_start, child_count, child_list, uniforms, bonus_u, temperature, res, \
+                     vr, accepted_slots, accepted_tokens, result)
+  if (V <= kSampThreads * 8) {
+    TM_SAMPLE_REG(8);
+  } else if (V <= kSampThreads * 16) {
+    TM_SAMPLE_REG(16);
+  } else if (V <= kSampRegMax) {
+    static_assert(kSampRegMax == kSampThreads * 32, "register kernel sizes");
+    TM_SAMPLE_REG(32);
+  } else {
+    hipLaunchKernelGGL(tm_sample_walk_tiled_kernel<kDtype>, dim3(1), dim3(kSampThreads), 0,
+                       stream, logits, N, V, row_stride, vl, q, q_stride, vq, tokens,
+                       child_start, child_count, child_list, uniforms, bonus_u, temperature, res,
+                       vr, accepted_slots, accepted_tokens, result);
+  }
+#undef TM_SAMPLE_REG
 }
 
 }  // namespace
@@ -545,17 +1001,29 @@ extern "C" int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V,
       num_prev > (1 << 24))
     return TM_ERR_SHAPE;
   if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
-  if (table_size < 2 * num_prev || (table_size & (table_size - 1)) != 0 || table_size > (1 << 26))
+  if (table_size < 2 * num_prev || table_size < kApplySlots ||
+      (table_size & (table_size - 1)) != 0 || table_size > (1 << 26))
     return TM_ERR_SHAPE;
   if (!(penalty > 0.0f)) return TM_ERR_ARG;
-  if (dtype == TM_DTYPE_F32) {
-    hipLaunchKernelGGL(tm_rep_penalty_kernel<TM_DTYPE_F32>, dim3(1), dim3(kPenThreads), 0,
-                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, prev_tokens,
-                       (int)num_prev, penalty, table, (int)table_size);
+  if (((uintptr_t)table % 16) != 0) return TM_ERR_ALIGN;
+  const hipStream_t s = (hipStream_t)stream;
+  const int S = (int)table_size;
+  if (S <= kPenLdsSlots) {
+    hipLaunchKernelGGL(tm_rep_count_kernel<true>, dim3(1), dim3(kPenThreads), 0, s, prev_tokens,
+                       (int)num_prev, (int)V, table, S);
   } else {
-    hipLaunchKernelGGL(tm_rep_penalty_kernel<TM_DTYPE_BF16>, dim3(1), dim3(kPenThreads), 0,
-                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, prev_tokens,
-                       (int)num_prev, penalty, table, (int)table_size);
+    hipLaunchKernelGGL(tm_rep_count_kernel<false>, dim3(1), dim3(kPenThreads), 0, s, prev_tokens,
+                       (int)num_prev, (int)V, table, S);
+  }
+  TM_HIP_CHECK_LAUNCH();
+  const dim3 grid((unsigned)N, (unsigned)std::min<int64_t>((S + kApplyBlock - 1) / kApplyBlock,
+                                                           4096));
+  if (dtype == TM_DTYPE_F32) {
+    hipLaunchKernelGGL(tm_rep_apply_kernel<TM_DTYPE_F32>, grid, dim3(kApplyThreads), 0, s,
+                       logits, row_stride, table, S, penalty);
+  } else {
+    hipLaunchKernelGGL(tm_rep_apply_kernel<TM_DTYPE_BF16>, grid, dim3(kApplyThreads), 0, s,
+                       logits, row_stride, table, S, penalty);
   }
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
@@ -569,20 +1037,20 @@ extern "C" int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int6
                                   float temperature, float* residual,
                                   int64_t* accepted_slots, int64_t* accepted_tokens,
                                   int64_t* result, void* stream) {
-  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || q_stride < V)
+  if (N < 1 || N > (1 << 20) || V < 1 || V > kSampMaxV || row_stride < V || q_stride < V)
     return TM_ERR_SHAPE;
   if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
   if (!(temperature > 0.0f)) return TM_ERR_ARG;
   if (dtype == TM_DTYPE_F32) {
-    hipLaunchKernelGGL(tm_sample_walk_kernel<TM_DTYPE_F32>, dim3(1), dim3(kSampThreads), 0,
-                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, draft_probs,
-                       q_stride, tokens, child_start, child_count, child_list, uniforms, bonus_u,
-                       temperature, residual, accepted_slots, accepted_tokens, result);
+    launch_sample_walk<TM_DTYPE_F32>(logits, (int)N, (int)V, row_stride, draft_probs, q_stride,
+                                     tokens, child_start, child_count, child_list, uniforms,
+                                     bonus_u, temperature, residual, accepted_slots,
+                                     accepted_tokens, result, (hipStream_t)stream);
   } else {
-    hipLaunchKernelGGL(tm_sample_walk_kernel<TM_DTYPE_BF16>, dim3(1), dim3(kSampThreads), 0,
-                       (hipStream_t)stream, logits, (int)N, (int)V, row_stride, draft_probs,
-                       q_stride, tokens, child_start, child_count, child_list, uniforms, bonus_u,
-                       temperature, residual, accepted_slots, accepted_tokens, result);
+    launch_sample_walk<TM_DTYPE_BF16>(logits, (int)N, (int)V, row_stride, draft_probs, q_stride,
+                                      tokens, child_start, child_count, child_list, uniforms,
+                                      bonus_u, temperature, residual, accepted_slots,
+                                      accepted_tokens, result, (hipStream_t)stream);
   }
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
