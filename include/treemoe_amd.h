@@ -153,7 +153,8 @@ int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
 
 /*
  * Gate/up projection + SwiGLU for many rows per expert (prefill / batched
- * trees), MFMA-tiled over 128 sorted rows x 128 weight rows.  Same maths as
+ * trees), MFMA-tiled over 128 sorted rows x (128 w1 + the same 128 w3) weight
+ * rows.  Same maths as
  * tm_op1_gemm1 and the reference `_moe_gemm1_kernel`
  * (treemoe/kernels/op1_tree_moe.py:300-383), but h is written ROW-MAJOR:
  *   h[p, n] = bf16( silu(x[sorted_slots[p] / 2] . w1[e, n]) * (... . w3[e, n]) )
@@ -161,7 +162,7 @@ int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
  * expert_offsets[e] .. expert_offsets[e+1]-1).  h: [2T, I] bf16 (rows >= 2T
  * untouched).  `tiles` is the 64-row tile list of the same routing: an expert
  * whose first tile entry is masked (expert -1) is skipped.  Requires
- * H % 64 == 0 and I % 64 == 0.  Consumed by tm_op1_prefill_gemm2.
+ * H % 64 == 0 and I % 128 == 0.  Consumed by tm_op1_prefill_gemm2.
  */
 int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w3, void* h,
                          const int32_t* sorted_slots, const int32_t* expert_offsets,
@@ -169,14 +170,14 @@ int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w3, void* h,
                          int64_t I, int64_t E, void* stream);
 
 /*
- * Down projection for many rows per expert, MFMA-tiled over 128 rows x 128
+ * Down projection for many rows per expert, MFMA-tiled over 128 rows x 256
  * output columns; the prefill counterpart of tm_op1_gemm2 (reference
  * `_moe_gemm2_det_kernel`, treemoe/kernels/op1_tree_moe.py:447-509):
  *   y[s, p, n] = gates_flat[sorted_slots[p]] * sum_{k in segment s} h[p, k] w2[e, n, k]
  * with h row-major [2T, I] from tm_op1_prefill_gemm1 and y [split, 2T, H] fp32
  * in the layout tm_op1_combine reads; masked experts (as in
  * tm_op1_prefill_gemm1) leave their rows of y untouched.  Requires
- * H % 128 == 0 and (I / split) % 64 == 0.
+ * H % 256 == 0 and (I / split) % 64 == 0.
  */
 int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y, const float* gates_flat,
                          const int32_t* sorted_slots, const int32_t* expert_offsets,

@@ -111,7 +111,8 @@ def test_tree_attention_plan():
     (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4000, 14336, 8, 0), 1001),  # H % 64
     (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 0, 2048, 4096, 14336, 8, 0), 1001),  # tiles
     (("tm_op1_prefill_gemm1", 8, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14336, 8, 0), 1002),  # align
-    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 2, 2048, 4032, 14336, 8, 0), 1001),  # H % 128
+    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 2, 2048, 4032, 14336, 8, 0), 1001),  # H % 256
+    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14272, 8, 0), 1001),  # I % 128
     (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 3, 2048, 4096, 14336, 8, 0), 1001),  # split
     (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1003),
     (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1001),
