@@ -22,11 +22,9 @@
 // fp32 sums before the (LDS-staged, coalesced) store of the partial y[segment].
 //
 // M-tiles are BM = 128 consecutive rows of one expert in the compact
-// expert-major order (expert_offsets).  Launch order: jobs (M-tile, column
-// block) in 8 x 8 super-blocks, M-tile fastest.  Workgroups are dealt to the
-// 8 XCDs in turn, so within a super-block each XCD takes one M-tile across 8
-// column blocks (its A rows come from that XCD's L2) while the 8 XCDs share
-// the same weight blocks through the Infinity Cache.
+// expert-major order (expert_offsets).  Launch order: workgroups are dealt
+// to the 8 XCDs in turn, and each XCD owns one eighth of the column jobs for
+// every M-tile, walked in super-blocks of 8 M-tiles x 4 columns (job_of).
 #pragma clang fp contract(off)
 
 #include "tm_common.h"
@@ -78,20 +76,31 @@ __device__ __forceinline__ int swz(int r, int c) {
   return r * PROW + ((c ^ ((r / RPB) & (CPR - 1))) << 4);
 }
 
-constexpr int SB = 8;  // super-block edge, in jobs
+constexpr int kXcds = 8;  // workgroup i runs on XCD i % 8
+constexpr int SBM = 8;    // super-block: M-tile slots (consecutive: mostly one expert) ..
+constexpr int SBN = 4;    // .. x column jobs, M fastest
 
-// Job of launch index i: M-tile slot and column job (both may be padding).
+// Job of launch index L: M-tile slot and column job (either may be padding,
+// which the kernels skip).  XCD x = L % 8 owns the column jobs
+// [x * cpx, (x + 1) * cpx) for every M-tile slot, so each weight block is read
+// through one XCD's L2 only, and walks them in SBM x SBN super-blocks: the
+// ~32 workgroups resident on the XCD share each A tile across SBN columns and
+// each weight block across the M-tiles of one expert.
 __device__ __forceinline__ void job_of(int L, int mt_max, int ncol, int* mt, int* col) {
-  const int nmb = (mt_max + SB - 1) / SB;
-  const int sb = L / (SB * SB), w = L - sb * (SB * SB);
-  const int sbm = sb % nmb, sbc = sb / nmb;
-  *mt = sbm * SB + (w % SB);
-  *col = sbc * SB + (w / SB);
+  const int x = L % kXcds, l = L / kXcds;
+  const int cpx = (ncol + kXcds - 1) / kXcds;
+  const int nsm = (mt_max + SBM - 1) / SBM;
+  const int sb = l / (SBM * SBN), w = l - sb * (SBM * SBN);
+  const int sbm = sb % nsm, sbn = sb / nsm;
+  *mt = sbm * SBM + w % SBM;
+  const int lc = sbn * SBN + w / SBM;  // column within the XCD's range
+  *col = lc < cpx ? x * cpx + lc : ncol;
 }
 
-// Launch size covering every (M-tile slot, column job) pair in super-blocks.
+// Launch size: 8 XCDs x every (M-tile slot, column) pair of one XCD's range.
 int64_t launch_jobs(int64_t mt_max, int64_t ncol) {
-  return ((mt_max + SB - 1) / SB) * ((ncol + SB - 1) / SB) * SB * SB;
+  const int64_t cpx = (ncol + kXcds - 1) / kXcds;
+  return kXcds * ((mt_max + SBM - 1) / SBM) * ((cpx + SBN - 1) / SBN) * SBM * SBN;
 }
 
 // M-tile `idx` of the compact expert-major order: expert, first row, rows.
@@ -138,23 +147,29 @@ __device__ __forceinline__ int dma_chunk(int row) {
   return (threadIdx.x & (CPR - 1)) ^ ((row / RPB) & (CPR - 1));
 }
 
-// Step `kstep` (K bytes 128 kstep ..) of both tiles into `st`; past the end
-// of K the loads are out of range and store zeros.  Always 6 loads per
-// thread, so the wait counts below stay exact.
-__device__ __forceinline__ void dma_step(const DmaLoad& d, uint8_t* st, int kstep, int nk) {
+// Load j (0 .. LDS_PER_STEP - 1: the A loads, then the B loads) of step
+// `kstep` (K bytes 128 kstep ..) of both tiles into `st`; past the end of K
+// the loads are out of range and store zeros.  Every step issues all
+// LDS_PER_STEP loads in this order, so the wait counts below stay exact.
+__device__ __forceinline__ void dma_one(const DmaLoad& d, uint8_t* st, int kstep, int nk, int j) {
   const uint32_t kb = (uint32_t)kstep * (uint32_t)PROW;
   const bool valid = kstep < nk;
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // LDS base: wave-uniform
-#pragma unroll
-  for (int i = 0; i < ALD; ++i)
+  if (j < ALD) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        d.ra, (lds_void*)(st + (8 * i + w) * 1024), 16,
-        (valid && d.aoff[i] != kOOR) ? d.aoff[i] + kb : kOOR, 0, 0, 0);
-#pragma unroll
-  for (int i = 0; i < BLD; ++i)
+        d.ra, (lds_void*)(st + (8 * j + w) * 1024), 16,
+        (valid && d.aoff[j] != kOOR) ? d.aoff[j] + kb : kOOR, 0, 0, 0);
+  } else {
+    const int i = j - ALD;
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         d.rb[i], (lds_void*)(st + ABYTES + (8 * i + w) * 1024), 16,
         valid ? d.boff[i] + kb : kOOR, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void dma_step(const DmaLoad& d, uint8_t* st, int kstep, int nk) {
+#pragma unroll
+  for (int j = 0; j < LDS_PER_STEP; ++j) dma_one(d, st, kstep, nk, j);
 }
 
 // Wait until at most n of this thread's vector-memory operations are
@@ -172,6 +187,8 @@ __device__ __forceinline__ u32x4_t frag(const uint8_t* tile, int row, int s, int
 }
 
 // acc[i][j] += A[64 wm + 32 i, :] B[brow[j], :]^T over one staged step.
+// (Spreading the next step's loads between this step's MFMAs instead of
+// issuing them before it measured no faster.)
 __device__ __forceinline__ void compute_step(const uint8_t* st, const int (&brow)[2],
                                              f32x16_t (&acc)[2][2]) {
   const int lane = threadIdx.x & 63;
