@@ -424,6 +424,32 @@ def test_mixtral_shape_configs(name):
     assert torch.equal(out, again)
 
 
+def test_reference_cpu_config_shape():
+    """The reference's CPU-runnable case (T=64, hidden 1024, FFN 3584, E=8,
+    top-2, no budget pruning; the configuration its treemoe/ref path is timed
+    on) run on the GPU: routing bit-exact against the C oracle, the output
+    within rel-L2 1e-2 of the fp64 CPU expert FFN, and deterministic."""
+    _say("reference CPU config shape on the GPU")
+    from treemoe_spec_amd.workloads import op1_workload
+
+    m = _op1()
+    inp = op1_workload("config1_cpu_small", device="cuda")
+    out = m.tree_moe_forward(inp.x, inp.w1, inp.w2, inp.w3, inp.router, inp.accept,
+                             inp.budget)
+    gates = oracle_c.router_gates(bf16_bits(inp.x), bf16_bits(inp.router))
+    ref = oracle_c.route_bucket(gates, inp.accept.cpu().numpy(), inp.budget)
+    routing = m.route_experts(inp.x, inp.router, inp.accept, inp.budget, inp.w1.shape[1])
+    assert np.array_equal(routing.topk_ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+    golden = op1_ref.expert_ffn_golden(inp.x.cpu(), inp.w1.cpu(), inp.w2.cpu(), inp.w3.cpu(),
+                                       torch.from_numpy(ref.topk_ids),
+                                       torch.from_numpy(ref.gates_flat))
+    err = op1_ref.rel_l2(out.double().cpu(), golden)
+    _say(f"  rel_l2={err:.3e}")
+    assert err <= REL_L2_TOL
+    assert torch.equal(out, m.tree_moe_forward(inp.x, inp.w1, inp.w2, inp.w3, inp.router,
+                                               inp.accept, inp.budget))
+
+
 def test_rejects_cpu_tensors_and_bad_dtypes():
     m = _op1()
     g = torch.Generator().manual_seed(0)
