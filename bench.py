@@ -263,6 +263,27 @@ def secondary(m, inp2, args) -> dict:
                      "tflops": round(fl / (ms * 1e-3) / 1e12, 2),
                      "pct_mfma_peak": round(100 * fl / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 2),
                      "active_experts": n_active}
+    # one GPU's share of a G-way tensor-parallel config-2 layer: I / G columns
+    # of w1/w3 and of w2 for all 8 experts (routing replicated; the rank-order
+    # reduce of the fp32 partials across GPUs is not part of this)
+    log("secondary tensor-parallel shares")
+    t, h, i, e = inp2.shape
+    shares = {}
+    for g in (2, 4, 8):
+        ig = i // g
+        w1 = inp2.w1[:, :ig, :].contiguous()
+        w3 = inp2.w3[:, :ig, :].contiguous()
+        w2 = inp2.w2[:, :, :ig].contiguous()
+        fwd = lambda: m.tree_moe_forward(inp2.x, w1, w2, w3, inp2.router, inp2.accept,
+                                         inp2.budget)
+        for _ in range(3):
+            fwd()
+        ms = events_time_ms(fwd, reps)
+        b = op1_algorithmic_bytes(t, h, ig, e, e)
+        shares[f"tp{g}_i{ig}"] = {"us": round(ms * 1e3, 2), "gbs": round(b / (ms * 1e-3) / 1e9, 1),
+                                  "pct_hbm_peak": round(100 * b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+        del w1, w2, w3
+    out["config2_tensor_parallel_share"] = shares
     log("secondary op4 config 4")
     w = op4_workload(n=64, vocab=32000, max_depth=8, seed=3)
     cfg = MixtralConfig()

@@ -219,6 +219,20 @@ def test_forward_token_counts(t):
     assert op1_ref.rel_l2(out.cpu().float(), golden) <= REL_L2_TOL
 
 
+def test_forward_tp8_share_shape():
+    """One GPU's share of an 8-way tensor-parallel Mixtral layer: I = 14336 / 8
+    = 1792 intermediate columns for all 8 experts at T = 64.  1792 / 2 is not a
+    multiple of 256, so the down GEMM runs unsplit (split 1)."""
+    _say("forward TP-8 share I=1792")
+    from treemoe_spec_amd.kernels.op1_tree_moe import _split_for
+
+    assert _split_for(1792) == 1
+    out, golden, _, _ = _forward_and_golden(64, 8, 4096, 1792, 8, 21, accept_kind="ones")
+    err = op1_ref.rel_l2(out.cpu().double(), golden)
+    _say(f"  rel_l2={err:.3e}")
+    assert err <= REL_L2_TOL
+
+
 def test_forward_degrade_branch():
     _say("forward degrade")
     m = _op1()
