@@ -130,16 +130,18 @@ struct WalkShared {
   int child_start[kStageNodes];
   int child_count[kStageNodes];
   int child_list[kStageNodes];
+  int next[kStageNodes];  // each node's accepted child, -1 if none
   int count;
 };
 
 // One workgroup: reduce the row partials to argmax[N], then the greedy walk
 // from the root (op4_commit.py:99-131): at each level take the first child,
 // in child-list order, whose token equals the node's argmax.  Trees of at
-// most kStageNodes nodes are staged in LDS first, so the walk's dependent
-// reads are LDS reads; larger trees are walked from global memory.  The walk
-// also stops once N nodes are accepted (only a child list with a cycle gets
-// there), so accepted_slots is never written past N.
+// most kStageNodes nodes are staged in LDS first and every node's accepted
+// child is found in parallel (one thread per node), so the serial walk is a
+// chase of one LDS read per level; larger trees are walked from global
+// memory.  The walk also stops once N nodes are accepted (only a child list
+// with a cycle gets there), so accepted_slots is never written past N.
 __global__ void __launch_bounds__(kWalkThreads)
 tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
                const int64_t* __restrict__ tokens, const int32_t* __restrict__ child_start,
@@ -159,14 +161,28 @@ tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
     }
     for (int i = tid; i < nlist; i += kWalkThreads) sh.child_list[i] = child_list[i];
   }
-  for (int row = wave; row < N; row += kWalkThreads / 64) {
+  // Row partials: lane l of a wave takes part l % P of row r0 + l / P, with
+  // P = parts rounded up to a power of two (<= 64), so one load per lane and
+  // log2(P) xor steps reduce 64 / P rows at once.  The ranking is a total
+  // order, so the order of the steps does not change the result.
+  static_assert(TM_OP4_MAX_PARTS <= 64, "a row's partials fit one wave");
+  int logp = 0;
+  while ((1 << logp) < parts) ++logp;
+  const int rows_per_wave = 64 >> logp;
+  for (int r0 = wave * rows_per_wave; r0 < N; r0 += (kWalkThreads / 64) * rows_per_wave) {
+    const int row = r0 + (lane >> logp);
+    const int p = lane & ((1 << logp) - 1);
     Best b{-INFINITY, 0x7fffffff};
-    for (int p = lane; p < parts; p += 64) {
+    if (row < N && p < parts) {
       const Partial q = partial[(size_t)row * parts + p];
       b.offer(q.v, q.i);
     }
-    b = wave_best(b);
-    if (lane == 0) {
+    for (int off = (1 << logp) >> 1; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(b.v, off);
+      const int oi = __shfl_xor(b.i, off);
+      b.offer(ov, oi);
+    }
+    if (p == 0 && row < N) {
       argmax[row] = b.i;
       if (staged) sh.argmax[row] = b.i;
     }
@@ -177,17 +193,35 @@ tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
   const int* cs = staged ? sh.child_start : child_start;
   const int* cc = staged ? sh.child_count : child_count;
   const int* cl = staged ? sh.child_list : child_list;
+  if (staged) {
+    for (int i = tid; i < N; i += kWalkThreads) {
+      const int64_t target = (int64_t)sh.argmax[i];
+      const int st = sh.child_start[i];
+      const int cnt = sh.child_count[i];
+      int acc = -1;
+      for (int j = 0; j < cnt; ++j) {
+        const int c = sh.child_list[st + j];
+        if (sh.tokens[c] == target) { acc = c; break; }
+      }
+      sh.next[i] = acc;
+    }
+    __syncthreads();
+  }
   if (tid == 0) {
     int node = 0;
     int count = 0;
     for (int d = 0; d < max_depth && count < N; ++d) {
-      const int64_t target = (int64_t)am[node];
-      const int st = cs[node];
-      const int cnt = cc[node];
       int acc = -1;
-      for (int j = 0; j < cnt; ++j) {
-        const int c = cl[st + j];
-        if (tok[c] == target) { acc = c; break; }
+      if (staged) {
+        acc = sh.next[node];
+      } else {
+        const int64_t target = (int64_t)am[node];
+        const int st = cs[node];
+        const int cnt = cc[node];
+        for (int j = 0; j < cnt; ++j) {
+          const int c = cl[st + j];
+          if (tok[c] == target) { acc = c; break; }
+        }
       }
       if (acc < 0) break;
       accepted_slots[count] = acc;
