@@ -193,10 +193,19 @@ def _forward_and_golden(t, e, h, i, budget, seed, objective="mass", accept_kind=
     return out, golden, (x, w1, w2, w3, router, accept), ref
 
 
+def _force_path(monkeypatch, path):
+    """Route tree_moe_forward through the weight-streaming GEMMs ("stream")
+    or the MFMA-tiled ones ("tiled") whatever the rows per expert."""
+    m = _op1()
+    monkeypatch.setattr(m, "TILED_MIN_ROWS", 1 << 30 if path == "stream" else 1)
+
+
+@pytest.mark.parametrize("path", ["stream", "tiled"])
 @pytest.mark.parametrize("budget", [2, 4, 8])
 @pytest.mark.parametrize("objective", ["mass", "critical_path"])
-def test_forward_matches_fp64_golden_small(budget, objective):
-    _say(f"forward small B={budget} {objective}")
+def test_forward_matches_fp64_golden_small(budget, objective, path, monkeypatch):
+    _say(f"forward small B={budget} {objective} {path}")
+    _force_path(monkeypatch, path)
     out, golden, inputs, ref = _forward_and_golden(64, 8, 512, 1024, budget, 5, objective)
     err = op1_ref.rel_l2(out.cpu().float(), golden)
     assert err <= REL_L2_TOL, err
@@ -279,10 +288,12 @@ def test_two_phase_equals_inline(budget):
     assert r is out and torch.equal(out, inline)
 
 
-def test_masked_expert_weights_never_read():
+@pytest.mark.parametrize("path", ["stream", "tiled"])
+def test_masked_expert_weights_never_read(path, monkeypatch):
     """NaN-poisoned weights of an expert that no token routes to must not leak
     (reference tests/test_op1.py:162-170)."""
-    _say("nan poison")
+    _say(f"nan poison {path}")
+    _force_path(monkeypatch, path)
     m = _op1()
     g = torch.Generator().manual_seed(1234)
     x, w1, w2, w3, router, _ = make_moe_inputs(64, 8, 256, 512, g, dtype=torch.float32)
@@ -297,8 +308,11 @@ def test_masked_expert_weights_never_read():
     assert not out.isnan().any()
 
 
-def test_exclude_experts_hybrid_matches_full():
+def test_exclude_experts_hybrid_matches_full(monkeypatch):
+    """Weight-streaming GEMMs (test_exclude_experts_tiled_path covers the tiled
+    ones)."""
     _say("exclude experts")
+    _force_path(monkeypatch, "stream")
     m = _op1()
     g = torch.Generator().manual_seed(23)
     x, w1, w2, w3, router, accept = make_moe_inputs(64, 8, 512, 1024, g, dtype=torch.bfloat16)

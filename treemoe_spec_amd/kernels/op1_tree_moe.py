@@ -49,8 +49,11 @@ def compact_block_capacity(num_slots: int, expert_budget: int, block_m: int = BM
 
 # Rows per active expert from which the MFMA-tiled GEMMs (128-row tiles that
 # reuse each weight tile across rows) replace the weight-streaming GEMMs
-# (one pass over an expert's weights per 64-row tile).
-TILED_MIN_ROWS = 128
+# (one pass over an expert's weights per 64-row tile).  Measured at the
+# Mixtral shape: 16 rows per expert (T=64, B=8) stream faster (501 vs 567 us),
+# from 32 (T=64, B=4 skewed; T=128, B=8) the tiled pair wins (306 vs 340 us,
+# 570 vs 598 us), and by 64 rows it takes 0.6x the streaming time.
+TILED_MIN_ROWS = 32
 
 
 def uses_tiled_gemms(num_tokens: int, expert_budget: int, num_experts: int) -> bool:
