@@ -170,7 +170,10 @@ struct Top2 {
 //     tile list, and the reference's padded BM-row block layout
 //     (op1_tree_moe.py:111-144) read back from the compact order.
 // Gates and accept are staged in LDS first and every intermediate stays in
-// LDS; global memory is written only with final values, each by one thread.
+// LDS; global memory is written only with final values, each by one thread,
+// and never read back here.  So the phases are separated by LDS-only barriers:
+// __syncthreads() would also wait for the phase's global stores to complete
+// (its workgroup release fence), measured at 0.5-1 us per phase.
 __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -198,7 +201,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   }
 #pragma unroll 8
   for (int t = tid; t < T; t += kThreads) sh.accept[t] = a.accept[t];
-  __syncthreads();
+  tm_lds_barrier();
   const float* G = staged ? sh.gates : a.gates;
 
   if (critical) {
@@ -209,7 +212,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
       sh.fe[2 * t] = (uint8_t)r.i1;
       sh.fe[2 * t + 1] = (uint8_t)r.i2;
     }
-    __syncthreads();
+    tm_lds_barrier();
   }
 
   // 1. demand (and criticality)
@@ -236,7 +239,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
       a.demand_out[e] = acc;
     }
   }
-  __syncthreads();
+  tm_lds_barrier();
 
   // 2. keep set (wave 0, lane = expert): rank in the order (crit desc,)
   //    demand desc, expert asc.
@@ -264,7 +267,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     const unsigned long long m = __ballot(kept != 0);
     if (lane == 0) sh.keep = m;
   }
-  __syncthreads();
+  tm_lds_barrier();
 
   // 3. in-budget top-2, renormalisation, low-acceptance degrade
   const unsigned long long keep = sh.keep;
@@ -283,7 +286,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     sh.fe[2 * t] = (uint8_t)r.i1;  // the critical-path use of fe ended at an earlier barrier
     sh.fe[2 * t + 1] = (uint8_t)r.i2;
   }
-  __syncthreads();
+  tm_lds_barrier();
 
   // 4a. per-chunk expert counts and in-chunk ranks from ballots
   for (int q = wave; q < nchunk; q += kWaves) {
@@ -298,7 +301,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     if (lane < E) sh.cnt[q * TM_MAX_EXPERTS + lane] = (uint16_t)mycnt;
     if (s < nslot) sh.inrank[s] = (uint8_t)inrank;
   }
-  __syncthreads();
+  tm_lds_barrier();
   // 4b. exclusive scan over chunks (slot order) per expert; chunks q and q+64
   //     of one expert sit in lane q of the wave that owns the expert.
   for (int e = wave; e < E; e += kWaves) {
@@ -311,7 +314,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     if (lane + 64 < nchunk) sh.cnt[(lane + 64) * TM_MAX_EXPERTS + e] = (uint16_t)(tot0 + x1);
     if (lane == 0) sh.count[e] = tot0 + tot1;
   }
-  __syncthreads();
+  tm_lds_barrier();
   // 4c. block layout (reference), compact offsets and GEMM tiles (wave 0,
   //     lane = expert)
   if (wave == 0) {
@@ -348,7 +351,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
       a.tiles[4 * j + 3] = 0;
     }
   }
-  __syncthreads();
+  tm_lds_barrier();
   // 4d. destinations of every slot, and the owner of every padded block
   for (int s = tid; s < nslot; s += kThreads) {
     const int fe = sh.fe[s];
@@ -368,7 +371,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     sh.owner[b] = (int16_t)owner;
     a.block_expert_ids[b] = owner;
   }
-  __syncthreads();
+  tm_lds_barrier();
   // 4e. padded rows: row i of block b holds the (i - first row of the owner)-th
   //     slot of the owning expert, or -1 past its count or in an unused block.
   for (int i = tid; i < padded_rows; i += kThreads) {

@@ -187,7 +187,14 @@ tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
       if (staged) sh.argmax[row] = b.i;
     }
   }
-  __syncthreads();
+  // A staged walk reads only LDS: an LDS-only barrier, which does not wait
+  // for the argmax stores.  Otherwise the walk reads argmax back from global
+  // memory, which needs __syncthreads()'s release/acquire.
+  if (staged) {
+    tm_lds_barrier();
+  } else {
+    __syncthreads();
+  }
   const int64_t* tok = staged ? sh.tokens : tokens;
   const int* am = staged ? sh.argmax : argmax;
   const int* cs = staged ? sh.child_start : child_start;
@@ -205,7 +212,7 @@ tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
       }
       sh.next[i] = acc;
     }
-    __syncthreads();
+    tm_lds_barrier();
   }
   if (tid == 0) {
     int node = 0;
@@ -234,7 +241,7 @@ tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
     result[1] = count;
     result[2] = node;
   }
-  __syncthreads();
+  tm_lds_barrier();  // sh.count; the padding below writes other entries
   for (int i = sh.count + tid; i < N; i += kWalkThreads) {
     accepted_slots[i] = -1;
     accepted_tokens[i] = -1;
