@@ -112,7 +112,6 @@ struct BucketShared {
   int block_start[TM_MAX_EXPERTS];
   int nblocks[TM_MAX_EXPERTS];
   int offset[TM_MAX_EXPERTS + 1];
-  unsigned long long keep;              // bit e: expert e is in the budget
   uint8_t fe[kMaxSlots];                // expert of slot s
   uint8_t inrank[kMaxSlots];            // rank of slot s among its expert's slots in its chunk
   uint16_t sorted[kMaxSlots];           // compact expert-major order
@@ -201,6 +200,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   }
 #pragma unroll 8
   for (int t = tid; t < T; t += kThreads) sh.accept[t] = a.accept[t];
+  for (int b = tid; b < a.max_blocks; b += kThreads) sh.owner[b] = -1;
   tm_lds_barrier();
   const float* G = staged ? sh.gates : a.gates;
 
@@ -241,40 +241,48 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   }
   tm_lds_barrier();
 
-  // 2. keep set (wave 0, lane = expert): rank in the order (crit desc,)
-  //    demand desc, expert asc.
-  if (wave == 0) {
-    int kept = 0;
-    if (lane < E) {
-      const float d = sh.demand[lane];
-      const float c = critical ? sh.crit[lane] : 0.0f;
-      int rank = 0;
-      for (int f = 0; f < E; ++f) {
-        const float df = sh.demand[f];
-        const float cf = critical ? sh.crit[f] : 0.0f;
-        bool before;
-        if (critical && cf != c) {
-          before = cf > c;
-        } else if (df != d) {
-          before = df > d;
-        } else {
-          before = f < lane;
-        }
-        rank += before ? 1 : 0;
+  // 2. keep set, computed by every wave (no barrier before step 3): lane =
+  //    expert, rank in the order (crit desc,) demand desc, expert asc, the
+  //    other experts' values read from their lanes (readlane, uniform index).
+  unsigned long long keep;
+  {
+    const float d = lane < E ? sh.demand[lane] : 0.0f;
+    const float c = (critical && lane < E) ? sh.crit[lane] : 0.0f;
+    int rank = 0;
+    for (int f = 0; f < E; ++f) {
+      const float df = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d), f));
+      const float cf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), f));
+      bool before;
+      if (critical && cf != c) {
+        before = cf > c;
+      } else if (df != d) {
+        before = df > d;
+      } else {
+        before = f < lane;
       }
-      kept = rank < a.budget ? 1 : 0;
+      rank += before ? 1 : 0;
     }
-    const unsigned long long m = __ballot(kept != 0);
-    if (lane == 0) sh.keep = m;
+    keep = __ballot(lane < E && rank < a.budget);
   }
-  tm_lds_barrier();
 
-  // 3. in-budget top-2, renormalisation, low-acceptance degrade
-  const unsigned long long keep = sh.keep;
+  // 3. in-budget top-2, renormalisation, low-acceptance degrade; the gate row
+  //    is read 4 experts at a time when its rows are 16-byte aligned
+  const bool vec_rows = (E & 3) == 0 && (reinterpret_cast<uintptr_t>(G) & 15) == 0;
   for (int t = tid; t < T; t += kThreads) {
     const float* g = G + (size_t)t * E;
     Top2 r{-1, -1, 0.0f, 0.0f};
-    for (int e = 0; e < E; ++e) r.offer(((keep >> e) & 1ull) ? g[e] : 0.0f, e);
+    if (vec_rows) {
+#pragma unroll 4
+      for (int e = 0; e < E; e += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(g + e);
+        r.offer(((keep >> e) & 1ull) ? v.x : 0.0f, e);
+        r.offer(((keep >> (e + 1)) & 1ull) ? v.y : 0.0f, e + 1);
+        r.offer(((keep >> (e + 2)) & 1ull) ? v.z : 0.0f, e + 2);
+        r.offer(((keep >> (e + 3)) & 1ull) ? v.w : 0.0f, e + 3);
+      }
+    } else {
+      for (int e = 0; e < E; ++e) r.offer(((keep >> e) & 1ull) ? g[e] : 0.0f, e);
+    }
     const float s = r.g1 + r.g2;
     float tg1 = r.g1 / s;
     float tg2 = r.g2 / s;
@@ -330,6 +338,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
       sh.block_start[lane] = bs;
       sh.nblocks[lane] = nb;
       a.expert_offsets[lane] = off;
+      for (int b = bs; b < min(bs + nb, a.max_blocks); ++b) sh.owner[b] = (int16_t)lane;
       for (int k = 0; k < nt; ++k) {
         const int j = ts + k;
         if (j < a.max_tiles) {
@@ -362,15 +371,7 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
     a.slot_pos[s] = pos;
     sh.sorted[pos] = (uint16_t)s;
   }
-  for (int b = tid; b < a.max_blocks; b += kThreads) {
-    int owner = -1;
-    for (int e = 0; e < E; ++e) {
-      if (sh.nblocks[e] > 0 && b >= sh.block_start[e] && b < sh.block_start[e] + sh.nblocks[e])
-        owner = e;
-    }
-    sh.owner[b] = (int16_t)owner;
-    a.block_expert_ids[b] = owner;
-  }
+  for (int b = tid; b < a.max_blocks; b += kThreads) a.block_expert_ids[b] = sh.owner[b];
   tm_lds_barrier();
   // 4e. padded rows: row i of block b holds the (i - first row of the owner)-th
   //     slot of the owning expert, or -1 past its count or in an unused block.
