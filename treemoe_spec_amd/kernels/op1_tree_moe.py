@@ -5,11 +5,14 @@ Same Python surface as the reference module treemoe/kernels/op1_tree_moe.py
 :81, ``Routing`` :568, ``route_experts`` :641, ``tree_moe_forward`` :711); the
 work runs in libtreemoe_amd.so:
 
-  routing      tm_op1_route          router (bf16 logits, fp32 softmax) + budget
-                                     routing + bucketing, one launch
+  routing      tm_op1_route          router (bf16 logits, fp32 softmax), then
+                                     budget routing + bucketing (two launches)
   gate/up      tm_op1_gemm1          MFMA, SwiGLU fused, h kept in bf16
   down         tm_op1_gemm2          MFMA, deterministic K split, gate applied
   combine      tm_op1_combine        fixed order, bf16 output
+
+At many rows per expert (uses_tiled_gemms) gate/up and down run as
+tm_op1_prefill_gemm1 / tm_op1_prefill_gemm2, MFMA-tiled over rows and weights.
 
 There is no CPU path: CPU tensors, other dtypes, or a missing library raise.
 """
@@ -29,8 +32,9 @@ if BM not in {16, 32}:
 
 # K segments of the down projection.  Each segment is one deterministic
 # partial; more segments = more, shorter workgroups and more partial traffic.
-# 2 is the measured optimum at the Mixtral shape on MI355X (1: 516 us,
-# 2: 497 us, 4: 517 us per layer at T=64, B=8).
+# Measured at the Mixtral shape on MI355X (T=64, B=8): 1 and 2 segments are
+# within 2 us per layer (478.5 and 476.8 us); 4 makes the down GEMM ~9 %
+# slower.
 SPLIT_K = 2
 TILE_M = TM_GEMM_TILE_M
 
