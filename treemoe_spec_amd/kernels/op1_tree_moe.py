@@ -72,6 +72,28 @@ def _split_for(inter: int) -> int:
     raise ValueError("intermediate size must be a multiple of 256")
 
 
+# The tiled down GEMM launches (real M-tiles) x (hidden / 256) x split jobs.
+# With few rows per layer (config 3: 4 experts, 128 rows) split 2 fills only
+# half the 256 CUs; 4 K segments fill one round: measured 120 -> 96 us at
+# T=64, B=4 (7 or 8 segments: 105-107 us).  Partials of 4 segments are kept
+# only where they are small.
+TILED_SPLIT_WIDE = 4
+_TILED_WIDE_MAX_BYTES = 64 << 20
+_CUS = 256
+
+
+def _tiled_split(n: int, expert_budget: int, num_experts: int, hidden: int, inter: int,
+                 ws: "_Workspace") -> int:
+    """K segments for the tiled down GEMM: TILED_SPLIT_WIDE when split 2 would
+    leave CUs idle and the workspace holds that many partials, else ws.split."""
+    s = TILED_SPLIT_WIDE
+    mtiles = -(-2 * n // 128) + min(expert_budget, num_experts)  # bound on real 128-row M-tiles
+    if (ws.partial.shape[0] >= s and inter % s == 0 and (inter // s) % 64 == 0
+            and mtiles * (hidden // 256) * ws.split < _CUS):
+        return s
+    return ws.split
+
+
 def _check_budget(expert_budget: int, num_experts: int, routing_objective: str) -> None:
     if not 2 <= expert_budget <= num_experts:
         raise ValueError(f"expert_budget must be in [2, {num_experts}]")
@@ -103,11 +125,14 @@ class _Workspace:
         self.num_experts = e
         self.rows = self.max_blocks * BM
         self.split = _split_for(inter)
+        # the tiled down GEMM may use more K segments at small shapes
+        wide = TILED_SPLIT_WIDE * 2 * n * hidden * 4 <= _TILED_WIDE_MAX_BYTES
+        nsplit = max(self.split, TILED_SPLIT_WIDE) if wide else self.split
         i32, i64, f32 = torch.int32, torch.int64, torch.float32
         self.router_gates = torch.empty(n, e, dtype=f32, device=device)
         # gate/up output, tile-swizzled: max_tiles x 64 rows x inter (A-fragment order)
         self.h = torch.empty(self.max_tiles * TILE_M, inter, dtype=dtype, device=device)
-        self.partial = torch.zeros(self.split, 2 * n, hidden, dtype=f32, device=device)
+        self.partial = torch.zeros(nsplit, 2 * n, hidden, dtype=f32, device=device)
         self.topk_flat = torch.zeros(2 * n, dtype=i64, device=device)
         self.gates_flat = torch.zeros(2 * n, dtype=f32, device=device)
         self.padded_slots = torch.full((self.rows,), -1, dtype=i64, device=device)
@@ -363,13 +388,15 @@ def tree_moe_forward(
             or routing.max_tiles > ws.max_tiles):
         raise ValueError("routing was computed for a different shape")
     stream = _capi.stream_of(x.device)
+    split = ws.split
     if uses_tiled_gemms(n, expert_budget, e):
+        split = _tiled_split(n, expert_budget, e, hidden, inter, ws)
         call("tm_op1_prefill_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h),
              ptr(routing.sorted_slots), ptr(routing.expert_offsets), ptr(routing.tiles),
              routing.max_tiles, n, hidden, inter, e, stream)
         call("tm_op1_prefill_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial),
              ptr(routing.gates_flat), ptr(routing.sorted_slots), ptr(routing.expert_offsets),
-             ptr(routing.tiles), routing.max_tiles, ws.split, n, hidden, inter, e, stream)
+             ptr(routing.tiles), routing.max_tiles, split, n, hidden, inter, e, stream)
     else:
         call("tm_op1_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h), ptr(routing.sorted_slots),
              ptr(routing.tiles), routing.max_tiles, n, hidden, inter, e, stream)
@@ -383,5 +410,5 @@ def tree_moe_forward(
     else:
         result = torch.empty_like(x)
     call("tm_op1_combine", ptr(ws.partial), ptr(routing.slot_pos), ptr(result), n, hidden,
-         ws.split, stream)
+         split, stream)
     return result
