@@ -87,6 +87,31 @@ def test_split_selection(inter, split):
         m._split_for(200)
 
 
+def test_tiled_down_gemm_split_rule():
+    """The tiled down GEMM takes 4 K segments when split 2 would launch less
+    than one round of 256 CUs (config 3), else the workspace's split (config
+    5); the partials of 4 segments are allocated only when small."""
+    from types import SimpleNamespace
+
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+
+    ws = m._Workspace(64, 8, 4096, 14336, "cpu", torch.bfloat16)  # config 2/3 shape
+    assert ws.split == 2 and ws.partial.shape == (4, 128, 4096)
+    # config 3: <= 1 + 4 real M-tiles x 16 column blocks x 2 = 160 jobs < 256
+    assert m._tiled_split(64, 4, 8, 4096, 14336, ws) == 4
+    # config 5: 32 + 8 M-tiles x 16 x 2 jobs fill the CUs; its partials stay at 2
+    big = SimpleNamespace(split=2, partial=torch.empty(2, 1, 1))
+    assert m._tiled_split(2048, 8, 8, 4096, 14336, big) == 2
+    wide = SimpleNamespace(split=2, partial=torch.empty(4, 1, 1))
+    assert m._tiled_split(2048, 8, 8, 4096, 14336, wide) == 2
+    # a workspace without room for 4 segments keeps its split
+    assert m._tiled_split(64, 4, 8, 4096, 14336, big) == 2
+    # 4 segments must keep (I / 4) % 64 == 0
+    assert m._tiled_split(64, 4, 8, 4096, 14336 + 128, wide) == 2
+    # large T: 4-segment partials would exceed the cap, so only 2 are allocated
+    assert m.TILED_SPLIT_WIDE * 2 * 4096 * 4096 * 4 > m._TILED_WIDE_MAX_BYTES
+
+
 def test_children_csr_packing():
     from treemoe_spec_amd.kernels.op4_commit import _children_csr
 
