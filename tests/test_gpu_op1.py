@@ -45,7 +45,11 @@ def _route_case(seed, t, e, h, budget, objective, accept_kind, block_m=16, route
 
 
 @pytest.mark.parametrize("t,h,e", [(1, 64, 8), (5, 512, 8), (64, 4096, 8), (64, 256, 2),
-                                   (33, 1024, 16), (2048, 4096, 8), (64, 512, 64)])
+                                   (33, 1024, 16), (2048, 4096, 8), (64, 512, 64),
+                                   # the row router (T >= 1024, W_g in LDS): ragged last
+                                   # workgroup, H = 2048 with E = 16; then a W_g too large
+                                   # for its LDS copy (one workgroup per token)
+                                   (1025, 4096, 8), (1100, 2048, 16), (1024, 4096, 16)])
 def test_router_gates_bit_exact(t, h, e):
     _say(f"router t={t} h={h} e={e}")
     m = _op1()

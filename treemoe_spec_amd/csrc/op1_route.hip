@@ -6,7 +6,8 @@
 // for bit: expert ids, gate weights, demand and every layout index.
 //
 // Launch shapes: the router runs one workgroup (8 waves) per token, one wave
-// per expert; the bucketing runs in one workgroup.  They are two launches:
+// per expert, or from 1024 tokens one wave per token with W_g in LDS; the
+// bucketing runs in one workgroup.  They are two launches:
 // handing the gates to a last-finishing workgroup instead would need a
 // device-scope release fence per workgroup (an L2 write-back), which measured
 // slower than the kernel boundary.
@@ -21,6 +22,11 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSlots = 2 * TM_MAX_TOKENS;
 constexpr int kMaxChunks = kMaxSlots / 64;
 constexpr int kMaxPaddedRows = 16384;
+// Tokens from which the row router runs: its per-workgroup W_g copy costs
+// ~8 us, so below ~1024 tokens one workgroup per token is faster (T = 512:
+// 6.1 against 8.6 us; T = 2048: 14.0 against 9.2 us; T = 4096: 25.4 against
+// 13.1 us at H = 4096, E = 8).
+constexpr int kRowsMinTokens = 1024;
 
 __device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -35,6 +41,20 @@ __device__ __forceinline__ float fma8(uint4 xv, uint4 wv, float acc) {
   acc = fmaf(lo_bf16(xv.w), lo_bf16(wv.w), acc);
   acc = fmaf(hi_bf16(xv.w), hi_bf16(wv.w), acc);
   return acc;
+}
+
+// Softmax of one token's E logits (s_logit, bf16-rounded) by one wave: max,
+// e^(l - max), a sum in expert order, a correctly rounded division.
+__device__ __forceinline__ void router_softmax(const float* s_logit, float* __restrict__ gates,
+                                               int t, int E, int lane) {
+  const float my_logit = (lane < E) ? s_logit[lane] : 0.0f;
+  float m = (lane < E) ? my_logit : -INFINITY;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+  const float ex = (lane < E) ? tm_expf_det(my_logit - m) : 0.0f;
+  float s = 0.0f;
+  for (int e = 0; e < E; ++e) s = s + __shfl(ex, e);
+  if (lane < E) gates[(size_t)t * E + lane] = ex / s;
 }
 
 // Router for token t in one workgroup.  Logit (t, e): lane l of the wave that
@@ -71,16 +91,7 @@ __device__ __forceinline__ void router_token(const uint16_t* __restrict__ x,
     if (lane == 0) s_logit[e] = tm_bf16_to_f32(tm_f32_to_bf16(acc));
   }
   __syncthreads();
-  if (wave == 0) {
-    const float my_logit = (lane < E) ? s_logit[lane] : 0.0f;
-    float m = (lane < E) ? my_logit : -INFINITY;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-    const float ex = (lane < E) ? tm_expf_det(my_logit - m) : 0.0f;
-    float s = 0.0f;
-    for (int e = 0; e < E; ++e) s = s + __shfl(ex, e);
-    if (lane < E) gates[(size_t)t * E + lane] = ex / s;
-  }
+  if (wave == 0) router_softmax(s_logit, gates, t, E, lane);
 }
 
 struct BucketArgs {
@@ -393,6 +404,64 @@ tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg
   router_token(x, wg, gates, blockIdx.x, H, E, s_logit);
 }
 
+// Router for many tokens: wave w of workgroup b takes token kWaves b + w and
+// all E experts.  x stays in registers (XC 16-byte chunks per lane, H = 512
+// XC) and W_g in LDS, read once per workgroup instead of once per token.  Lane
+// l accumulates its chunks l, l+64, ... of each expert in the order
+// router_token uses, then the same xor fold, rounding and softmax, so the
+// gates are bit-identical to it.
+constexpr int kRowsLdsChunks = 4096;  // W_g staged in LDS: E * H / 8 <= 4096 (64 KB)
+
+template <int XC>
+__global__ void __launch_bounds__(kThreads)
+tm_router_rows_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
+                      float* __restrict__ gates, int T, int H, int E) {
+  __shared__ uint4 s_w[kRowsLdsChunks];
+  __shared__ float s_logit[kWaves][TM_MAX_EXPERTS];
+  const int nchunk = H >> 3;  // = 64 XC
+  const uint4* wg4 = reinterpret_cast<const uint4*>(wg);
+  for (int i = threadIdx.x; i < E * nchunk; i += kThreads) s_w[i] = wg4[i];
+  tm_lds_barrier();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * kWaves + wave;
+  if (t >= T) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)t * H);
+  uint4 xv[XC];
+#pragma unroll
+  for (int u = 0; u < XC; ++u) xv[u] = xr[lane + 64 * u];
+  for (int e = 0; e < E; ++e) {
+    const uint4* wr = s_w + e * nchunk;
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < XC; ++u) acc = fma8(xv[u], wr[lane + 64 * u], acc);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
+    if (lane == 0) s_logit[wave][e] = tm_bf16_to_f32(tm_f32_to_bf16(acc));
+  }
+  // s_logit[wave] is written and read by this wave only: its LDS operations
+  // complete in order
+  router_softmax(s_logit[wave], gates, t, E, lane);
+}
+
+// Launch the router: the row kernel when W_g fits its LDS copy, H is one of
+// its register shapes and there are enough tokens to fill the chip with
+// workgroups of kWaves tokens; otherwise one workgroup per token.
+void launch_router(const uint16_t* x, const uint16_t* wg, float* gates, int T, int H, int E,
+                   hipStream_t stream) {
+  const bool rows_ok = T >= kRowsMinTokens && E * (H / 8) <= kRowsLdsChunks;
+  const dim3 rgrid((unsigned)((T + kWaves - 1) / kWaves));
+  if (rows_ok && H == 2048) {
+    hipLaunchKernelGGL(tm_router_rows_kernel<4>, rgrid, dim3(kThreads), 0, stream, x, wg, gates,
+                       T, H, E);
+  } else if (rows_ok && H == 4096) {
+    hipLaunchKernelGGL(tm_router_rows_kernel<8>, rgrid, dim3(kThreads), 0, stream, x, wg, gates,
+                       T, H, E);
+  } else {
+    hipLaunchKernelGGL(tm_router_kernel, dim3((unsigned)T), dim3(kThreads), 0, stream, x, wg,
+                       gates, T, H, E);
+  }
+}
+
 __global__ void __launch_bounds__(kThreads) tm_bucket_kernel(BucketArgs args) {
   __shared__ __attribute__((aligned(16))) BucketShared sh;
   bucket_all(args, sh);
@@ -445,9 +514,8 @@ extern "C" int tm_op1_router_gates(const void* x, const void* wg, int64_t T, int
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS || H < 8 || (H % 8) != 0)
     return TM_ERR_SHAPE;
   if (((uintptr_t)x % 16) != 0 || ((uintptr_t)wg % 16) != 0) return TM_ERR_ALIGN;
-  hipLaunchKernelGGL(tm_router_kernel, dim3((unsigned)T), dim3(kThreads), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)wg, gates, (int)T,
-                     (int)H, (int)E);
+  launch_router((const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E,
+                (hipStream_t)stream);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
@@ -487,9 +555,8 @@ extern "C" int tm_op1_route(const void* x, const void* wg, const float* accept, 
                                  max_tiles, topk_ids, gates_flat, padded_slots,
                                  block_expert_ids, slot_to_row, demand, expert_offsets,
                                  sorted_slots, slot_pos, tiles);
-  hipLaunchKernelGGL(tm_router_kernel, dim3((unsigned)T), dim3(kThreads), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)wg, gates, (int)T,
-                     (int)H, (int)E);
+  launch_router((const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E,
+                (hipStream_t)stream);
   TM_HIP_CHECK_LAUNCH();
   hipLaunchKernelGGL(tm_bucket_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, a);
   TM_HIP_CHECK_LAUNCH();
