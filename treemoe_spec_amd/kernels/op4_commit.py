@@ -32,7 +32,6 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
-import numpy as np
 import torch
 
 from treemoe_spec_amd import _capi
@@ -77,18 +76,22 @@ def _apply_rep_penalty(logits: torch.Tensor, dtype: int, prev_tokens, rep_penalt
 
 
 def _children_csr(children: list[list[int]], n: int, device) -> torch.Tensor:
-    """[starts | counts | flat] int32 in one host->device copy."""
+    """[starts | counts | flat] int32 in one host->device copy, from pinned
+    memory and ordered on the current stream (no host synchronisation)."""
     if len(children) != n:
         raise ValueError(f"children must list {n} nodes, got {len(children)}")
-    counts = np.fromiter((len(c) for c in children), dtype=np.int64, count=n)
-    flat = [c for kids in children for c in kids]
+    starts, counts, flat = [], [], []
+    for kids in children:
+        starts.append(len(flat))
+        counts.append(len(kids))
+        flat.extend(kids)
     if flat and (min(flat) < 0 or max(flat) >= n):
         raise ValueError("child index out of range")
-    starts = np.zeros(n, dtype=np.int64)
-    if n > 1:
-        starts[1:] = np.cumsum(counts)[:-1]
-    packed = np.concatenate([starts, counts, np.asarray(flat or [0], dtype=np.int64)])
-    return torch.from_numpy(packed.astype(np.int32)).to(device, non_blocking=False)
+    packed = starts + counts + (flat or [0])
+    if torch.device(device).type != "cuda":
+        return torch.tensor(packed, dtype=torch.int32)
+    host = torch.tensor(packed, dtype=torch.int32, pin_memory=True)
+    return host.to(device, non_blocking=True)
 
 
 def _tree_depth(children: list[list[int]]) -> int:

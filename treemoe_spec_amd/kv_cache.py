@@ -95,12 +95,15 @@ class PagedKVCache:
     def device_tables(self, device) -> tuple[torch.Tensor, torch.Tensor]:
         """int32 copies of block_table and the scratch page list on ``device``,
         refreshed only when the block table has grown."""
+        device = torch.device(device)
+        if device.type == "cuda" and device.index is None:
+            device = torch.device("cuda", torch.cuda.current_device())
         if self._dev_table is None or self._dev_table_len != len(self.block_table) \
-                or self._dev_table.device != torch.device(device):
+                or self._dev_table.device != device:
             self._dev_table = torch.tensor(self.block_table or [0], dtype=torch.int32,
                                            device=device)
             self._dev_table_len = len(self.block_table)
-        if self._dev_scratch is None or self._dev_scratch.device != torch.device(device):
+        if self._dev_scratch is None or self._dev_scratch.device != device:
             self._dev_scratch = torch.tensor(self.tree_pages, dtype=torch.int32, device=device)
         return self._dev_table, self._dev_scratch
 
