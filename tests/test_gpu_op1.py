@@ -388,6 +388,24 @@ def test_tiled_and_streaming_gemms_agree(monkeypatch):
     assert op1_ref.rel_l2(tiled.float().cpu(), streaming.float().cpu()) <= 5e-3
 
 
+def test_tiled_down_gemm_segment_counts_agree(monkeypatch):
+    """The tiled path at a small shape takes 4 K segments for the down GEMM;
+    forced back to 2 it must give the same layer up to fp32 summation order,
+    and both must meet the fp64 golden."""
+    _say("tiled down GEMM, 2 vs 4 K segments")
+    m = _op1()
+    _force_path(monkeypatch, "tiled")
+    out4, golden, inputs, _ = _forward_and_golden(64, 8, 512, 1024, 4, 21)
+    ws = next(w for k, w in m._ws_cache.items() if k[:4] == (64, 8, 512, 1024))
+    assert m._tiled_split(64, 4, 8, 512, 1024, ws) == 4
+    assert op1_ref.rel_l2(out4.cpu().float(), golden) <= REL_L2_TOL
+    monkeypatch.setattr(m, "TILED_SPLIT_WIDE", 2)
+    dev = [a.cuda() for a in inputs]
+    out2 = m.tree_moe_forward(*dev, 4)
+    assert op1_ref.rel_l2(out2.cpu().float(), golden) <= REL_L2_TOL
+    assert op1_ref.rel_l2(out2.float().cpu(), out4.float().cpu()) <= 2e-3
+
+
 def test_exclude_experts_tiled_path():
     _say("exclude experts, tiled")
     m = _op1()
