@@ -46,23 +46,47 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def events_time_ms(fn, reps: int) -> float:
-    """Mean wall time of fn() on the current stream, HIP events."""
+def step_times_ms(fn, reps: int) -> list[float]:
+    """Per-call device time of fn() for `reps` back-to-back calls: one HIP
+    event pair per call on the current stream (the stream the library
+    launches on)."""
     import torch
 
-    s = torch.cuda.Event(enable_timing=True)
-    e = torch.cuda.Event(enable_timing=True)
-    s.record()
-    for _ in range(reps):
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for s, e in ev:
+        s.record()
         fn()
-    e.record()
-    e.synchronize()
-    return s.elapsed_time(e) / reps
+        e.record()
+    ev[-1][1].synchronize()
+    return [s.elapsed_time(e) for s, e in ev]
+
+
+def median(xs: list[float]) -> float:
+    ys = sorted(xs)
+    n = len(ys)
+    return ys[n // 2] if n % 2 else 0.5 * (ys[n // 2 - 1] + ys[n // 2])
+
+
+def events_time_ms(fn, reps: int) -> float:
+    """Median per-call device time of fn() over `reps` calls (HIP events)."""
+    return median(step_times_ms(fn, reps))
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def kernel_breakdown(m, inp, reps: int) -> dict:
-    """Average duration (ms) of each launch of one op1 step, events placed on
-    the stream the library launches on (torch's current stream)."""
+    """Median duration (ms) of each launch of one op1 step over `reps` steps,
+    events placed on the stream the library launches on (torch's current
+    stream)."""
     import torch
 
     from treemoe_spec_amd import _capi
@@ -95,7 +119,7 @@ def kernel_breakdown(m, inp, reps: int) -> dict:
     torch.cuda.synchronize()
     res = {}
     for k, name in enumerate(names):
-        res[name] = sum(ev[r][k].elapsed_time(ev[r][k + 1]) for r in range(reps)) / reps
+        res[name] = median([ev[r][k].elapsed_time(ev[r][k + 1]) for r in range(reps)])
     return res
 
 
@@ -136,8 +160,8 @@ def cpu_baseline(inp, budget_s: float, bytes_alg: int) -> dict:
         "kind": "port",
         "sample": (f"{len(times)} full config-2 layers (T=64, H=4096, I=14336, E=8, B=8) "
                    f"through the torch CPU restatement of treemoe/ref/tree_moe_ref.py; "
-                   f"median {med * 1e3:.1f} ms/layer; host {platform.processor() or platform.machine()}, "
-                   f"os.cpu_count()={threads}"),
+                   f"median {med * 1e3:.1f} ms/layer; host CPU {cpu_model()}, "
+                   f"os.cpu_count()={threads}, torch threads {torch.get_num_threads()}"),
         "ms_per_layer": round(med * 1e3, 3),
     }
 
@@ -178,16 +202,23 @@ def main():
     log(f"timing {args.steps} steps")
     torch.cuda.synchronize()
     w0 = time.perf_counter()
-    ms = events_time_ms(fwd, args.steps)
+    times = step_times_ms(fwd, args.steps)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - w0) * 1e3 / args.steps
+    ms = median(times)
+    mean_ms = sum(times) / len(times)
 
-    bd = kernel_breakdown(m, inp, args.steps)
+    # per-launch breakdown: median over at least 50 steps after 10 more warm-ups
+    reps = max(args.steps, 50)
+    for _ in range(10):
+        fwd()
+    bd = kernel_breakdown(m, inp, reps)
     # algorithmic bytes per launch: one read of the active experts' weights
-    # (w1 + w3 for gemm1, w2 for gemm2) and of the activations in and out
-    gemm1_bytes = n_active * 2 * h * i * 2 + t * h * 2 + 2 * t * i * 2
+    # (w1 + w3 for gemm1, w2 for gemm2) plus the activation rows in (x); the
+    # h and fp32-partial workspaces are not counted
+    gemm1_bytes = n_active * 2 * h * i * 2 + t * h * 2
     gemm1_gbs = gemm1_bytes / (bd["gemm1"] * 1e-3) / 1e9
-    gemm2_bytes = n_active * h * i * 2 + 2 * t * i * 2 + m._split_for(i) * 2 * t * h * 4
+    gemm2_bytes = n_active * h * i * 2
     gemm2_gbs = gemm2_bytes / (bd["gemm2"] * 1e-3) / 1e9
     traffic = measured_traffic(ROOT / "profiles" / "op1_gemm1_config2_pmc.txt")
     value = bytes_alg / (ms * 1e-3) / 1e9
@@ -201,6 +232,10 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
         "us_per_layer": round(ms * 1e3, 2),
+        "timing": {"statistic": "median of the timed steps (one HIP event pair per step)",
+                   "mean_us": round(mean_ms * 1e3, 2), "min_us": round(min(times) * 1e3, 2),
+                   "max_us": round(max(times) * 1e3, 2),
+                   "breakdown_steps": reps},
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -214,7 +249,9 @@ def main():
                      "achieved": round(gemm1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemm1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_alg_per_launch": gemm1_bytes,
-                     "avg_launch_us": round(bd["gemm1"] * 1e3, 2)},
+                     "bytes_alg_unit": "w1 + w3 row pair (2 x H x 2 B = 16 KiB) x I x "
+                                       "active experts, plus x (T x H x 2 B)",
+                     "median_launch_us": round(bd["gemm1"] * 1e3, 2)},
         "kernels_us": {k: round(v * 1e3, 2) for k, v in bd.items()},
         "gemm2_gbs": round(gemm2_gbs, 1),
         "wall_ms_per_step": round(wall_ms, 4),
@@ -310,7 +347,7 @@ def secondary(m, inp2, args) -> dict:
 
     dev = logits.device
     n, v = logits.shape
-    csr = op4_commit._children_csr(w.children, n, dev)
+    csr, num_edges = op4_commit._children_csr(w.children, n, dev)
     am = torch.empty(n, dtype=torch.int32, device=dev)
     slots = torch.empty(n, dtype=torch.int64, device=dev)
     toks = torch.empty(n, dtype=torch.int64, device=dev)
@@ -323,7 +360,8 @@ def secondary(m, inp2, args) -> dict:
     def device_step():
         _capi.call("tm_op4_argmax_walk", logits.data_ptr(), _capi.TM_DTYPE_BF16, n, v,
                    logits.stride(0), tokens.data_ptr(), csr.data_ptr(), csr.data_ptr() + 4 * n,
-                   csr.data_ptr() + 8 * n, 8, am.data_ptr(), slots.data_ptr(), toks.data_ptr(),
+                   csr.data_ptr() + 8 * n, num_edges, 8, 0, am.data_ptr(), slots.data_ptr(),
+                   toks.data_ptr(),
                    result.data_ptr(), wsp.data_ptr(), stream)
         _capi.call("tm_op4_kv_commit", k.data_ptr(), kv.v.data_ptr(), k.element_size(),
                    k.shape[0], k.shape[3] * k.shape[4], k.stride(0), k.stride(1), k.stride(2),
@@ -366,7 +404,8 @@ def secondary(m, inp2, args) -> dict:
     def sample_step():
         _capi.call("tm_op4_sample_walk", logits.data_ptr(), _capi.TM_DTYPE_BF16, n, v,
                    logits.stride(0), q.data_ptr(), q.stride(0), tokens.data_ptr(), csr.data_ptr(),
-                   csr.data_ptr() + 4 * n, csr.data_ptr() + 8 * n, uni.data_ptr(), bu.data_ptr(),
+                   csr.data_ptr() + 4 * n, csr.data_ptr() + 8 * n, num_edges, uni.data_ptr(),
+                   bu.data_ptr(),
                    1.0, resid.data_ptr(), slots.data_ptr(), toks.data_ptr(), result.data_ptr(),
                    stream)
 

@@ -196,8 +196,16 @@ int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y, const float* g
  * logits: [N, V] (row stride `row_stride` elements), dtype TM_DTYPE_F32 or
  * TM_DTYPE_BF16.  NaN ranks above every number (first NaN wins), as in
  * torch.argmax.  tokens [N] i64; children in CSR form: child_start [N] i32,
- * child_count [N] i32, child_list [max(1, N-1)] i32.  The walk visits at most
- * max_depth levels (and accepts at most N nodes).
+ * child_count [N] i32, child_list [max(1, num_edges)] i32 holding num_edges
+ * entries (N - 1 for a full tree, fewer when the tree is padded with
+ * edge-free slots).  Child ranges are clipped to num_edges and children
+ * outside [0, N) never match.  The walk visits at most max_depth levels (and
+ * accepts at most N nodes).
+ * softmax_argmax = 0: argmax of the logits (reference :203-206).
+ * softmax_argmax = 1: argmax of softmax(row) rounded to the logits' dtype, the
+ * reference's pick when a repetition penalty was applied (:207-214): with
+ * e_i = exp(x_i - max), s = sum e_i, the first i whose rounded e_i / s equals
+ * the rounded 1 / s (one workgroup per row instead of the row ranges).
  * Outputs: argmax [N] i32, accepted_slots [N] i64 (-1 pad), accepted_tokens
  * [N] i64 (-1 pad), result [3] i64 = (bonus_token, num_accepted, next_root).
  * `workspace`: N * TM_OP4_MAX_PARTS * 8 bytes of device memory, 8-byte
@@ -206,8 +214,9 @@ int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y, const float* g
 int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
                        int64_t row_stride, const int64_t* tokens,
                        const int32_t* child_start, const int32_t* child_count,
-                       const int32_t* child_list, int64_t max_depth,
-                       int32_t* argmax, int64_t* accepted_slots,
+                       const int32_t* child_list, int64_t num_edges,
+                       int64_t max_depth, int softmax_argmax, int32_t* argmax,
+                       int64_t* accepted_slots,
                        int64_t* accepted_tokens, int64_t* result,
                        void* workspace, void* stream);
 
@@ -239,15 +248,17 @@ int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V, int64_t ro
  * unbounded (at most N accepted nodes).  When every child is rejected (or at a
  * leaf) the bonus token is the smallest j with residual[0] + .. + residual[j] >
  * bonus_u[0] * sum (inverse CDF; the reference calls torch.multinomial).
- * draft_probs: [N, V] fp32, row stride q_stride.  uniforms [N], bonus_u [1]
+ * draft_probs: [N, V] fp32, row stride q_stride.  Children in CSR form with
+ * num_edges entries, as in tm_op4_argmax_walk.  uniforms [N], bonus_u [1]
  * fp32 on the device.  residual: V fp32 of device memory (the final residual
  * on return).  V <= 2^25.  Outputs as tm_op4_argmax_walk.
  */
 int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int64_t V, int64_t row_stride,
                        const float* draft_probs, int64_t q_stride, const int64_t* tokens,
                        const int32_t* child_start, const int32_t* child_count,
-                       const int32_t* child_list, const float* uniforms, const float* bonus_u,
-                       float temperature, float* residual, int64_t* accepted_slots,
+                       const int32_t* child_list, int64_t num_edges, const float* uniforms,
+                       const float* bonus_u, float temperature, float* residual,
+                       int64_t* accepted_slots,
                        int64_t* accepted_tokens, int64_t* result, void* stream);
 
 /*

@@ -74,24 +74,38 @@ static float fold64(float* s) {
   return s[0];
 }
 
+/* bf16 bits of the router logit x[t] . wg[e]: 64 lane partials over 8-element
+ * chunks (chunk c to lane c % 64, fused multiply-adds in chunk order), the
+ * pairwise fold, then round to bf16. */
+static uint16_t router_logit_bits(const uint16_t* x, const uint16_t* wg, int64_t t, int64_t e,
+                                  int64_t H) {
+  float part[ORC_LANES];
+  for (int l = 0; l < ORC_LANES; ++l) part[l] = 0.0f;
+  for (int64_t c = 0; c < H / 8; ++c) {
+    const int l = (int)(c % ORC_LANES);
+    for (int j = 0; j < 8; ++j) {
+      const float a = bf16_bits_to_f32(x[t * H + 8 * c + j]);
+      const float b = bf16_bits_to_f32(wg[e * H + 8 * c + j]);
+      part[l] = fmaf(a, b, part[l]);
+    }
+  }
+  return f32_to_bf16_bits(fold64(part));
+}
+
+/* logits[t, e] (bf16 bits) as the router computes them before the softmax */
+void orc_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t H, int64_t E,
+                       uint16_t* logits) {
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t e = 0; e < E; ++e) logits[t * E + e] = router_logit_bits(x, wg, t, e, H);
+}
+
 /* gates[t, e] = softmax(bf16(x[t] . wg[e])) */
 void orc_router_gates(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t H, int64_t E,
                       float* gates) {
   float logits[64];
   for (int64_t t = 0; t < T; ++t) {
-    for (int64_t e = 0; e < E; ++e) {
-      float part[ORC_LANES];
-      for (int l = 0; l < ORC_LANES; ++l) part[l] = 0.0f;
-      for (int64_t c = 0; c < H / 8; ++c) {
-        const int l = (int)(c % ORC_LANES);
-        for (int j = 0; j < 8; ++j) {
-          const float a = bf16_bits_to_f32(x[t * H + 8 * c + j]);
-          const float b = bf16_bits_to_f32(wg[e * H + 8 * c + j]);
-          part[l] = fmaf(a, b, part[l]);
-        }
-      }
-      logits[e] = bf16_bits_to_f32(f32_to_bf16_bits(fold64(part)));
-    }
+    for (int64_t e = 0; e < E; ++e)
+      logits[e] = bf16_bits_to_f32(router_logit_bits(x, wg, t, e, H));
     float m = -INFINITY;
     for (int64_t e = 0; e < E; ++e) m = fmaxf(m, logits[e]);
     float ex[64];
@@ -266,6 +280,46 @@ void orc_argmax(const void* logits, int dtype, int64_t N, int64_t V, int64_t row
  * child in list order whose token equals the node's argmax is accepted.
  * result = (bonus, num_accepted, next_root).
  */
+/*
+ * Argmax of softmax(row) rounded to the row's dtype (the reference's greedy
+ * pick after a repetition penalty: _postprocess_softmax_kernel at temperature 1
+ * then _argmax_kernel over the probabilities, treemoe/kernels/op4_commit.py:
+ * 207-214).  e_i = exp(x_i - max); the sum s runs in 256 index-strided partials
+ * (partial j adds elements j, j+256, ... in order), each 64 partials folded
+ * pairwise, the 4 folds added in order; p_i = round(e_i / s).  Returns the
+ * first i with p_i equal to the row maximum's p = round(1 / s); 0 if none.
+ */
+void orc_softmax_argmax(const void* logits, int dtype, int64_t N, int64_t V,
+                        int64_t row_stride, int32_t* out) {
+  for (int64_t n = 0; n < N; ++n) {
+    const float* pf = (const float*)logits + n * row_stride;
+    const uint16_t* pb = (const uint16_t*)logits + n * row_stride;
+#define ORC_X(i) (dtype == 0 ? pf[i] : bf16_bits_to_f32(pb[i]))
+#define ORC_ROUND(p) (dtype == 0 ? (p) : bf16_bits_to_f32(f32_to_bf16_bits(p)))
+    float m = -INFINITY;
+    for (int64_t i = 0; i < V; ++i) m = fmaxf(m, ORC_X(i));
+    float part[4 * ORC_LANES];
+    for (int j = 0; j < 4 * ORC_LANES; ++j) part[j] = 0.0f;
+    for (int64_t i = 0; i < V; ++i) {
+      const int j = (int)(i % (4 * ORC_LANES));
+      part[j] = part[j] + orc_expf(ORC_X(i) - m);
+    }
+    float s = fold64(part);
+    for (int w = 1; w < 4; ++w) s = s + fold64(part + w * ORC_LANES);
+    const float top = ORC_ROUND(1.0f / s);
+    int32_t first = 0;
+    for (int64_t i = 0; i < V; ++i) {
+      if (ORC_ROUND(orc_expf(ORC_X(i) - m) / s) == top) {
+        first = (int32_t)i;
+        break;
+      }
+    }
+    out[n] = first;
+#undef ORC_X
+#undef ORC_ROUND
+  }
+}
+
 void orc_greedy_walk(const int32_t* argmax, const int64_t* tokens, const int32_t* child_start,
                      const int32_t* child_count, const int32_t* child_list, int64_t N,
                      int64_t max_depth, int64_t* accepted_slots, int64_t* accepted_tokens,

@@ -20,6 +20,23 @@ import torch
 import torch.nn.functional as F
 
 
+def keep_set(gates: torch.Tensor, accept: torch.Tensor, expert_budget: int,
+             top1_threshold: float = 0.05, routing_objective: str = "mass") -> torch.Tensor:
+    """The experts op3 keeps (tree_moe_ref.py:34-49), in keep order."""
+    e = gates.shape[1]
+    demand = (accept.unsqueeze(1) * gates).sum(0)
+    by_demand = torch.argsort(demand, descending=True, stable=True)
+    if routing_objective == "critical_path":
+        full = gates.topk(2, dim=-1).indices
+        axis = torch.arange(e, device=gates.device)
+        need = (full[:, :1] == axis) | (
+            (full[:, 1:2] == axis) & (accept >= top1_threshold).unsqueeze(1))
+        crit = torch.where(need, accept.unsqueeze(1), -torch.inf).amax(0)
+        return by_demand[torch.argsort(crit[by_demand], descending=True,
+                                       stable=True)[:expert_budget]]
+    return by_demand[:expert_budget]
+
+
 def budget_route(gates: torch.Tensor, accept: torch.Tensor, expert_budget: int,
                  top1_threshold: float = 0.05, routing_objective: str = "mass"):
     """op3: acceptance-weighted expert budget, masked top-2, renorm, degrade.
@@ -30,18 +47,7 @@ def budget_route(gates: torch.Tensor, accept: torch.Tensor, expert_budget: int,
         raise ValueError(f"expert_budget must be in [2, {e}]")
     if routing_objective not in ("mass", "critical_path"):
         raise ValueError("routing_objective must be 'mass' or 'critical_path'")
-    demand = (accept.unsqueeze(1) * gates).sum(0)
-    by_demand = torch.argsort(demand, descending=True, stable=True)
-    if routing_objective == "critical_path":
-        full = gates.topk(2, dim=-1).indices
-        axis = torch.arange(e, device=gates.device)
-        need = (full[:, :1] == axis) | (
-            (full[:, 1:2] == axis) & (accept >= top1_threshold).unsqueeze(1))
-        crit = torch.where(need, accept.unsqueeze(1), -torch.inf).amax(0)
-        keep = by_demand[torch.argsort(crit[by_demand], descending=True,
-                                       stable=True)[:expert_budget]]
-    else:
-        keep = by_demand[:expert_budget]
+    keep = keep_set(gates, accept, expert_budget, top1_threshold, routing_objective)
     kept = torch.zeros(e, dtype=torch.bool, device=gates.device)
     kept[keep] = True
     w, ids = gates.masked_fill(~kept, 0.0).topk(2, dim=-1)

@@ -31,11 +31,15 @@ def _load():
         lib.orc_expf.argtypes = [ctypes.c_float]
         lib.orc_router_gates.restype = None
         lib.orc_router_gates.argtypes = [P, P, I64, I64, I64, P]
+        lib.orc_router_logits.restype = None
+        lib.orc_router_logits.argtypes = [P, P, I64, I64, I64, P]
         lib.orc_route_bucket.restype = ctypes.c_int
         lib.orc_route_bucket.argtypes = [P, P, I64, I64, I64, ctypes.c_float, ctypes.c_int,
                                          I64, I64, I64] + [P] * 10
         lib.orc_argmax.restype = None
         lib.orc_argmax.argtypes = [P, ctypes.c_int, I64, I64, I64, P]
+        lib.orc_softmax_argmax.restype = None
+        lib.orc_softmax_argmax.argtypes = [P, ctypes.c_int, I64, I64, I64, P]
         lib.orc_greedy_walk.restype = None
         lib.orc_greedy_walk.argtypes = [P, P, P, P, P, I64, I64, P, P, P]
         lib.orc_kv_commit.restype = None
@@ -68,6 +72,18 @@ def router_gates(x_bf16_bits: np.ndarray, wg_bf16_bits: np.ndarray) -> np.ndarra
     assert w.shape[1] == h and h % 8 == 0 and e <= 64
     out = np.empty((t, e), dtype=np.float32)
     _load().orc_router_gates(_ptr(x), _ptr(w), t, h, e, _ptr(out))
+    return out
+
+
+def router_logits(x_bf16_bits: np.ndarray, wg_bf16_bits: np.ndarray) -> np.ndarray:
+    """bf16 bits (uint16) of the router logits [T, E] behind router_gates."""
+    x = np.ascontiguousarray(x_bf16_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(wg_bf16_bits, dtype=np.uint16)
+    t, h = x.shape
+    e = w.shape[0]
+    assert w.shape[1] == h and h % 8 == 0
+    out = np.empty((t, e), dtype=np.uint16)
+    _load().orc_router_logits(_ptr(x), _ptr(w), t, h, e, _ptr(out))
     return out
 
 
@@ -130,6 +146,16 @@ def argmax(logits: np.ndarray, bf16_bits: bool = False) -> np.ndarray:
     n, v = x.shape
     out = np.empty(n, np.int32)
     _load().orc_argmax(_ptr(x), 1 if bf16_bits else 0, n, v, v, _ptr(out))
+    return out
+
+
+def softmax_argmax(logits: np.ndarray, bf16_bits: bool = False) -> np.ndarray:
+    """Per row, the first index of the maximum of softmax(row) rounded to the
+    row's dtype (fp32, or bf16 when ``bf16_bits``)."""
+    x = np.ascontiguousarray(logits, dtype=np.uint16 if bf16_bits else np.float32)
+    n, v = x.shape
+    out = np.empty(n, np.int32)
+    _load().orc_softmax_argmax(_ptr(x), 1 if bf16_bits else 0, n, v, v, _ptr(out))
     return out
 
 

@@ -114,8 +114,10 @@ def test_tree_attention_plan():
     (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 2, 2048, 4032, 14336, 8, 0), 1001),  # H % 256
     (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14272, 8, 0), 1001),  # I % 128
     (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 3, 2048, 4096, 14336, 8, 0), 1001),  # split
-    (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1003),
-    (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0), 1001),
+    (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 3, 1, 0, 0, 0, 0, 0, 0, 0), 1003),
+    (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 3, 1, 0, 0, 0, 0, 0, 0, 0), 1001),
+    (("tm_op4_argmax_walk", 0, 0, 4, 10, 10, 0, 0, 0, 0, -1, 1, 0, 0, 0, 0, 0, 0, 0), 1001),
+    (("tm_op4_argmax_walk", 0, 0, 4, 10, 10, 0, 0, 0, 0, 3, 1, 2, 0, 0, 0, 0, 0, 0), 1003),
     (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 0, 1.5, 0, 16, 0), 1001),     # no tokens
     (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 1.5, 0, 12, 0), 1001),     # table size
     (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 1.5, 0, 4, 0), 1001),      # table < 2n
@@ -123,12 +125,14 @@ def test_tree_attention_plan():
     (("tm_op4_rep_penalty", 0, 5, 4, 10, 10, 0, 4, 1.5, 0, 16, 0), 1003),     # dtype
     (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 1, 1.5, 0, 2, 0), 1001),      # table < 4
     (("tm_op4_rep_penalty", 0, 0, 4, 10, 10, 0, 4, 1.5, 8, 16, 0), 1002),     # table align
-    (("tm_op4_sample_walk", 0, 0, 4, (1 << 25) + 1, 1 << 26, 0, 1 << 26, 0, 0, 0, 0, 0, 0, 1.0,
-      0, 0, 0, 0, 0), 1001),                                                    # V > 2^25
-    (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 10, 0, 0, 0, 0, 0, 0, 0.0, 0, 0, 0, 0, 0),
+    (("tm_op4_sample_walk", 0, 0, 4, (1 << 25) + 1, 1 << 26, 0, 1 << 26, 0, 0, 0, 0, 3, 0, 0,
+      1.0, 0, 0, 0, 0, 0), 1001),                                               # V > 2^25
+    (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 10, 0, 0, 0, 0, 3, 0, 0, 0.0, 0, 0, 0, 0, 0),
      1003),                                                                     # temperature
-    (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 9, 0, 0, 0, 0, 0, 0, 1.0, 0, 0, 0, 0, 0),
+    (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 9, 0, 0, 0, 0, 3, 0, 0, 1.0, 0, 0, 0, 0, 0),
      1001),                                                                     # q stride
+    (("tm_op4_sample_walk", 0, 0, 4, 10, 10, 0, 10, 0, 0, 0, 0, -1, 0, 0, 1.0, 0, 0, 0, 0, 0),
+     1001),                                                                     # num_edges
 ])
 def test_argument_errors_return_before_launch(call, expect):
     from treemoe_spec_amd import _capi

@@ -173,3 +173,34 @@ def test_rejects_bad_inputs():
         tree_attention(q.float().cuda(), k.cuda(), v.cuda(), kv, 0, mask.cuda())
     with pytest.raises(ValueError, match="multiple"):
         tree_attention(q[:, :3].contiguous().cuda(), k.cuda(), v.cuda(), kv, 0, mask.cuda())
+
+
+def test_reference_cache_layout():
+    """A cache with exactly the reference PagedKVCache attributes (page 64,
+    scratch block ``tree_block``, no tree_pages / device_tables): the
+    attention and its write_tree match the oracle."""
+    _say("tree attention through the reference cache layout")
+    from tests.ref_layout_cache import RefLayoutKVCache
+    from treemoe_spec_amd.kernels.tree_attention import tree_attention
+
+    n, hq, kvh, seq_len = 64, 16, 4, 700
+    g = torch.Generator().manual_seed(21)
+    kv = RefLayoutKVCache(2, kvh, 128, seq_len // 64 + 5, device="cuda", dtype=torch.bfloat16)
+    kv.k.copy_(torch.randn(kv.k.shape, generator=g).to(torch.bfloat16))
+    kv.v.copy_(torch.randn(kv.v.shape, generator=g).to(torch.bfloat16))
+    perm = torch.randperm(len(kv._free), generator=g).tolist()
+    kv._free = [kv._free[i] for i in perm]
+    kv._ensure_capacity(seq_len)
+    kv.seq_len = seq_len
+    q = (torch.randn(n, hq, 128, generator=g) * 3).to(torch.bfloat16)
+    k = torch.randn(n, kvh, 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(n, kvh, 128, generator=g).to(torch.bfloat16)
+    parent = [-1] + [int(torch.randint(0, i, (1,), generator=g)) for i in range(1, n)]
+    mask = attn_ref.ancestor_mask(parent)
+    want = attn_ref.tree_attention(q, k, v, kv.k.cpu(), kv.v.cpu(), 1, kv.block_table,
+                                   seq_len, 64, mask)
+    out = tree_attention(q.cuda(), k.cuda(), v.cuda(), kv, 1, mask.cuda())
+    torch.cuda.synchronize()
+    _check(out, want)
+    assert torch.equal(kv.k[1, kv.tree_block, :n].cpu(), k)
+    assert torch.equal(kv.v[1, kv.tree_block, :n].cpu(), v)

@@ -77,12 +77,12 @@ def _direct_argmax(logits, argmax):
     n, v = logits.shape
     dtype = _capi.TM_DTYPE_F32 if logits.dtype == torch.float32 else _capi.TM_DTYPE_BF16
     tokens = torch.zeros(n, dtype=torch.long, device="cuda")
-    csr = _children_csr([[] for _ in range(n)], n, "cuda")
+    csr, edges = _children_csr([[] for _ in range(n)], n, "cuda")
     out = [torch.empty(n, dtype=torch.long, device="cuda") for _ in range(2)]
     result = torch.empty(3, dtype=torch.long, device="cuda")
     _capi.call("tm_op4_argmax_walk", logits.data_ptr(), dtype, n, v, logits.stride(0),
                tokens.data_ptr(), csr.data_ptr(), csr.data_ptr() + 4 * n,
-               csr.data_ptr() + 8 * n, 0, argmax.data_ptr(), out[0].data_ptr(),
+               csr.data_ptr() + 8 * n, edges, 0, 0, argmax.data_ptr(), out[0].data_ptr(),
                out[1].data_ptr(), result.data_ptr(),
                argmax_workspace(n, logits.device).data_ptr(), _capi.stream_of(logits.device))
 
@@ -267,14 +267,14 @@ def _direct_sample(logits, q, tokens, children, uniforms, bonus_u, temperature):
 
     n, v = logits.shape
     assert q.shape == (n, v) and tokens.numel() == n and uniforms.numel() >= n
-    csr = _children_csr(children, n, "cuda")
+    csr, edges = _children_csr(children, n, "cuda")
     slots = torch.empty(n, dtype=torch.int64, device="cuda")
     toks = torch.empty(n, dtype=torch.int64, device="cuda")
     result = torch.empty(3, dtype=torch.int64, device="cuda")
     residual = torch.empty(v, dtype=torch.float32, device="cuda")
     p = _capi.ptr
     _capi.call("tm_op4_sample_walk", p(logits), _dt(logits), n, v, logits.stride(0), p(q),
-               q.stride(0), p(tokens), p(csr), p(csr) + 4 * n, p(csr) + 8 * n, p(uniforms),
+               q.stride(0), p(tokens), p(csr), p(csr) + 4 * n, p(csr) + 8 * n, edges, p(uniforms),
                p(bonus_u), float(temperature), p(residual), p(slots), p(toks), p(result),
                _capi.stream_of(logits.device))
     torch.cuda.synchronize()
@@ -371,7 +371,7 @@ def test_sampling_first_token_distribution():
     from treemoe_spec_amd import _capi
     from treemoe_spec_amd.kernels.op4_commit import _children_csr
 
-    csr = _children_csr(children, 4, "cuda")
+    csr, edges = _children_csr(children, 4, "cuda")
     slots = torch.empty(trials, 4, dtype=torch.int64, device="cuda")
     toks = torch.empty(trials, 4, dtype=torch.int64, device="cuda")
     result = torch.empty(trials, 3, dtype=torch.int64, device="cuda")
@@ -380,7 +380,7 @@ def test_sampling_first_token_distribution():
     stream = _capi.stream_of(logits.device)
     for t in range(trials):
         _capi.call("tm_op4_sample_walk", P(logits), _dt(logits), 4, v, v, P(q), v,
-                   P(tokens[t]), P(csr), P(csr) + 16, P(csr) + 32, P(u[t]), P(bu[t]),
+                   P(tokens[t]), P(csr), P(csr) + 16, P(csr) + 32, edges, P(u[t]), P(bu[t]),
                    temperature, P(residual), P(slots[t]), P(toks[t]), P(result[t]), stream)
     torch.cuda.synchronize()
     num = result[:, 1].cpu()
@@ -484,11 +484,145 @@ def test_greedy_with_rep_penalty(dtype):
             op4_ref.rep_penalty_inplace(want, prev_arg if prev_arg is not None
                                         else torch.zeros(1, dtype=torch.long), penalty)
         assert torch.equal(lg.cpu(), want)
-        r_slots, _, r_bonus, r_num = op4_ref.tree_verify(want.float(), None, tokens, children)
+        if penalty != 1.0:
+            # the reference's pick after a penalty: argmax of the rounded softmax
+            am = (oracle_c.softmax_argmax(bf16_bits(want), bf16_bits=True)
+                  if dtype == torch.bfloat16 else oracle_c.softmax_argmax(want.numpy()))
+        else:
+            am = oracle_c.argmax(want.float().numpy())
+        r_slots, _, r_bonus, r_num, _ = oracle_c.greedy_walk(am, tokens.numpy(), children, 6)
         assert int(res.num_accepted) == r_num and int(res.bonus_token) == r_bonus
-        assert torch.equal(res.accepted_slots.cpu(), r_slots)
+        assert np.array_equal(res.accepted_slots.cpu().numpy(), r_slots)
     # with the penalty on token 10 the walk takes node 2 (token 11) instead
     lg = logits.clone().cuda()
     res = op4.fused_verify_commit(lg, None, tokens.cuda(), None, children, rep_penalty=1.5,
                                   prev_tokens=prev.cuda())
     assert res.accepted_slots[:1].tolist() == [2]
+
+
+# ------------------------------------------- reference cache and padded trees --
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_commit_through_reference_cache_layout(dtype):
+    """fused_verify_commit with a cache that has exactly the reference
+    PagedKVCache attributes (page 64, scratch block ``tree_block``, no
+    tree_pages / device_tables), fp32 logits as the engine passes them
+    (loop.py:185): committed bytes equal the oracle's commit_tree."""
+    _say(f"commit through reference cache layout {dtype}")
+    from tests.ref_layout_cache import RefLayoutKVCache
+    from treemoe_spec_amd.workloads import op4_workload
+
+    op4 = _op4()
+    n, seq_len = 64, 1000
+    for seed in (11, 12, 13):
+        w = op4_workload(n=n, vocab=4096, max_depth=8, seed=seed)
+        kv = RefLayoutKVCache(4, 2, 64, (seq_len + 80) // 64 + 4, device="cuda", dtype=dtype)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        kv.k.normal_(generator=g)
+        kv.v.normal_(generator=g)
+        perm = torch.randperm(len(kv._free), generator=torch.Generator().manual_seed(seed))
+        kv._free = [kv._free[i] for i in perm.tolist()]
+        kv._ensure_capacity(seq_len)
+        kv.seq_len = seq_len
+        k0, v0 = kv.k.clone(), kv.v.clone()
+        res = op4.fused_verify_commit(w.logits.float().cuda(), None, w.tokens.cuda(),
+                                      w.parent.cuda(), w.children, kv=kv, max_depth=8)
+        torch.cuda.synchronize()
+        num = int(res.num_accepted)
+        assert kv.seq_len == seq_len + num + 1
+        commit = torch.cat([torch.zeros(1, dtype=torch.long), res.accepted_slots.cpu()])
+        assert op4_ref.commit_tree(k0, v0, commit, [kv.tree_block], kv.block_table,
+                                   seq_len) == num + 1
+        assert torch.equal(kv.k, k0) and torch.equal(kv.v, v0)
+        ref_slots, _, ref_bonus, ref_num = op4_ref.tree_verify(w.logits.float(), None,
+                                                               w.tokens, w.children)
+        assert ref_num == num and int(res.bonus_token) == ref_bonus
+        assert torch.equal(res.accepted_slots.cpu(), ref_slots)
+
+
+def _padded_tree(seed, n, num_valid, vocab):
+    """A num_valid-node random tree in slots 0..num_valid-1 and edge-free
+    padding slots after it, as the engine builds trees smaller than
+    tree_size (engine/tree.py:175-188)."""
+    g, parent, children, tokens, _ = _tree(seed, num_valid, vocab)
+    children = [list(c) for c in children] + [[] for _ in range(n - num_valid)]
+    tokens = torch.cat([tokens, torch.zeros(n - num_valid, dtype=tokens.dtype)])
+    parent = torch.cat([parent, torch.full((n - num_valid,), -1, dtype=parent.dtype)])
+    return g, parent, children, tokens
+
+
+@pytest.mark.parametrize("seed,num_valid", [(0, 40), (1, 1), (2, 63), (3, 17)])
+def test_padded_tree_greedy(seed, num_valid):
+    _say(f"padded tree greedy seed={seed} valid={num_valid}")
+    op4 = _op4()
+    n, v = 64, 2048
+    g, parent, children, tokens = _padded_tree(seed, n, num_valid, v)
+    logits = torch.randn(n, v, generator=g) * 3
+    for node in range(num_valid):
+        if children[node] and node % 2 == 0:
+            logits[node, tokens[children[node][0]]] += 100.0
+    ref = op4_ref.tree_verify(logits, None, tokens, children)
+    res = op4.fused_verify_commit(logits.cuda(), None, tokens.cuda(), parent.cuda(), children,
+                                  max_depth=n)
+    assert int(res.num_accepted) == ref[3] and int(res.bonus_token) == ref[2]
+    assert torch.equal(res.accepted_slots.cpu(), ref[0])
+    assert torch.equal(res.accepted_tokens.cpu(), ref[1])
+
+
+@pytest.mark.parametrize("seed,num_valid", [(4, 40), (5, 2)])
+def test_padded_tree_sampling(seed, num_valid):
+    _say(f"padded tree sampling seed={seed} valid={num_valid}")
+    n, v = 64, 1000
+    g, parent, children, tokens = _padded_tree(seed, n, num_valid, v)
+    logits = torch.randn(n, v, generator=g)
+    q = torch.softmax(torch.randn(n, v, generator=g), -1)
+    uniforms = torch.rand(n, generator=g) * 0.3
+    bonus_u = torch.rand(1, generator=g)
+    slots, toks, result, _ = _direct_sample(logits.cuda(), q.cuda(), tokens.cuda(), children,
+                                            uniforms.cuda(), bonus_u.cuda(), 1.0)
+    r_slots, r_toks, r_bonus, r_num = op4_ref.tree_verify(
+        logits, q, tokens, children, temperature=1.0, uniforms=uniforms,
+        bonus_uniform=float(bonus_u))
+    assert int(result[1]) == r_num and int(result[0]) == r_bonus
+    assert torch.equal(slots, r_slots) and torch.equal(toks, r_toks)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_softmax_argmax_matches_oracle(dtype):
+    """The argmax of the rounded softmax (greedy + repetition penalty) is
+    bit-exact against the oracle: config-4 rows, unaligned rows, planted ties
+    whose rounded probabilities are equal (the lower index wins although its
+    logit is smaller), a row of -inf."""
+    _say(f"softmax argmax {dtype}")
+    from treemoe_spec_amd import _capi
+    from treemoe_spec_amd.kernels.op4_commit import _children_csr, argmax_workspace
+
+    g = torch.Generator().manual_seed(23)
+    for n, v in ((64, 32000), (5, 1001), (3, 7)):
+        x = torch.randn(n, v, generator=g) * 3
+        if v > 100:
+            x[0] = -10.0
+            x[0, 5], x[0, 7] = 0.0, 1e-9
+            x[1] = -3.0
+            x[1, 3], x[1, 9] = 2.0 ** -8, 2.0 ** -8 + 2.0 ** -15
+            x[2] = -float("inf")
+        x = x.to(dtype)
+        if dtype == torch.bfloat16:
+            want = oracle_c.softmax_argmax(bf16_bits(x), bf16_bits=True)
+        else:
+            want = oracle_c.softmax_argmax(x.numpy())
+        if v > 100:
+            assert want[0] == 5 and want[1] == 3 and want[2] == 0
+        xd = x.cuda()
+        tokens = torch.zeros(n, dtype=torch.long, device="cuda")
+        csr, edges = _children_csr([[] for _ in range(n)], n, "cuda")
+        argmax = torch.empty(n, dtype=torch.int32, device="cuda")
+        out = [torch.empty(n, dtype=torch.long, device="cuda") for _ in range(2)]
+        result = torch.empty(3, dtype=torch.long, device="cuda")
+        _capi.call("tm_op4_argmax_walk", xd.data_ptr(), _dt(xd), n, v, xd.stride(0),
+                   tokens.data_ptr(), csr.data_ptr(), csr.data_ptr() + 4 * n,
+                   csr.data_ptr() + 8 * n, edges, 0, 1, argmax.data_ptr(), out[0].data_ptr(),
+                   out[1].data_ptr(), result.data_ptr(),
+                   argmax_workspace(n, xd.device).data_ptr(), _capi.stream_of(xd.device))
+        torch.cuda.synchronize()
+        assert np.array_equal(argmax.cpu().numpy(), want), (n, v)

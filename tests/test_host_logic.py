@@ -116,8 +116,16 @@ def test_children_csr_packing():
     from treemoe_spec_amd.kernels.op4_commit import _children_csr
 
     children = [[1, 2], [3], [], []]
-    csr = _children_csr(children, 4, "cpu").tolist()
+    csr, edges = _children_csr(children, 4, "cpu")
+    csr = csr.tolist()
     assert csr[:4] == [0, 2, 3, 3] and csr[4:8] == [2, 1, 0, 0] and csr[8:] == [1, 2, 3]
+    assert edges == 3
+    # a tree padded with edge-free slots (the engine's num_valid < N) has fewer
+    # than N - 1 edges, and the count says so
+    csr, edges = _children_csr([[1], [], [], []], 4, "cpu")
+    assert edges == 1 and csr.tolist()[8:] == [1]
+    csr, edges = _children_csr([[], [], [], []], 4, "cpu")
+    assert edges == 0 and csr.tolist()[8:] == [0]
     with pytest.raises(ValueError):
         _children_csr([[5], [], [], []], 4, "cpu")
     with pytest.raises(ValueError):
@@ -211,3 +219,110 @@ def test_moe_adapter_host_logic(monkeypatch):
     calls.clear()
     fn(torch.zeros(3, 8), lw, 1)
     assert torch.equal(calls[0][1], torch.ones(3)) and calls[0][2] == 3
+
+
+def test_kv_cache_append_gather_commit_tree():
+    """The product cache carries the reference cache's model-facing methods
+    (append, gather, gather_with_tail, commit_tree; treemoe/model/kv_cache.py:62-145)
+    with the multi-page tree scratch."""
+    from treemoe_spec_amd.kv_cache import MixtralConfig, PagedKVCache
+
+    cfg = MixtralConfig(num_layers=2, num_kv_heads=2, head_dim=4)
+    kv = PagedKVCache(cfg, 16, device="cpu", dtype=torch.float32, page_size=16, tree_size=40)
+    kv._free = kv._free[::-1]          # a non-identity page order
+    g = torch.Generator().manual_seed(0)
+    rows = torch.randn(37, 2, 4, generator=g)
+    kv.append(1, rows[:20], rows[:20] + 1, 0)
+    kv.append(1, rows[20:], rows[20:] + 1, 20)
+    assert kv.seq_len == 37
+    k, v = kv.gather(1)
+    assert torch.equal(k, rows) and torch.equal(v, rows + 1)
+    tail = torch.randn(5, 2, 4, generator=g)
+    fk, fv = kv.gather_with_tail(1, tail, tail - 1)
+    assert torch.equal(fk, torch.cat([rows, tail])) and torch.equal(fv, torch.cat([rows + 1, tail - 1]))
+    tree = torch.randn(40, 2, 4, generator=g)
+    for layer in range(2):
+        kv.write_tree(layer, tree + layer, tree - layer)
+    kv.commit_tree(torch.tensor([0, 5, 17, 39, -1, -1]))
+    assert kv.seq_len == 41
+    for layer in (0, 1):
+        k, v = kv.gather(layer)
+        assert torch.equal(k[37:], tree[[0, 5, 17, 39]] + layer)
+        assert torch.equal(v[37:], tree[[0, 5, 17, 39]] - layer)
+    assert torch.equal(kv.gather(1)[0][:37], rows)
+    # an empty prefix
+    kv.reset()
+    fk, _ = kv.gather_with_tail(0, tail, tail)
+    assert torch.equal(fk, tail)
+
+
+def test_op4_commit_host_logic_with_reference_cache(monkeypatch):
+    """op4's commit glue on an object with exactly the reference cache's
+    attributes (tree_block, page 64, no tree_pages / device_tables): the
+    launch gets scratch page [tree_block], the block table after the
+    reference's capacity growth (op4_commit.py:251) and seq_len; replaying the
+    launch with the oracle commits [root] + path to seq_len, seq_len + 1, ..."""
+    from oracle import op4_ref
+    from tests.ref_layout_cache import RefLayoutKVCache
+    from treemoe_spec_amd.kernels import op4_commit
+
+    kv = RefLayoutKVCache(2, 2, 8, 6, device="cpu", dtype=torch.float32)
+    kv.k.normal_(generator=torch.Generator().manual_seed(1))
+    kv.v.normal_(generator=torch.Generator().manual_seed(2))
+    kv._ensure_capacity(100)
+    kv.seq_len = 100
+    k0, v0 = kv.k.clone(), kv.v.clone()
+    seen = {}
+
+    def fake_call(name, *args):
+        seen["name"], seen["args"] = name, args
+
+    monkeypatch.setattr(op4_commit, "call", fake_call)
+    slots = torch.tensor([3, 9, 30] + [-1] * 61)
+    result = torch.tensor([7, 3, 30])
+    op4_commit._commit(kv, slots, result, 64, 6, torch.device("cpu"), 0)
+    assert seen["name"] == "tm_op4_kv_commit"
+    a = seen["args"]
+    assert a[8] == 64 and a[12] == 1 and a[14] == len(kv.block_table) and a[15] == 100
+    assert a[16] == 6 and len(kv.block_table) * 64 >= 100 + 7
+    table, scratch = op4_commit.device_tables_of(kv, "cpu")
+    assert scratch.tolist() == [kv.tree_block] and table.tolist() == kv.block_table
+    # replay what the kernel does with the oracle
+    commit = torch.cat([torch.zeros(1, dtype=torch.long), slots])
+    assert op4_ref.commit_tree(k0, v0, commit, scratch.tolist(), table.tolist(), 100) == 4
+    for j, s in enumerate([0, 3, 9, 30]):
+        blk, off = kv.slot_of(100 + j)
+        assert torch.equal(k0[:, blk, off], kv.k[:, 0, s])
+    # the table cache follows the host table
+    kv._ensure_capacity(300)
+    table2, _ = op4_commit.device_tables_of(kv, "cpu")
+    assert table2.tolist() == kv.block_table
+    with pytest.raises(ValueError, match="scratch"):
+        op4_commit._commit(kv, slots, result, 65, 6, torch.device("cpu"), 0)
+
+
+def test_routing_token_count_mismatch_raises_before_launch(monkeypatch):
+    """A Routing computed for T tokens cannot be used with x of another T
+    (same tile count: T=64 and T=65 both bound 9 tiles)."""
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+
+    def no_launch(*a, **k):
+        raise AssertionError("launched")
+
+    monkeypatch.setattr(m, "call", no_launch)
+    monkeypatch.setattr(m, "_require_device", lambda *t: None)
+    e, h, i = 8, 256, 256
+    ws = m._Workspace(64, e, h, i, "cpu", torch.bfloat16)
+    ws65 = m._Workspace(65, e, h, i, "cpu", torch.bfloat16)
+    assert ws.max_tiles == ws65.max_tiles
+    r = m.Routing(ws, ws.router_gates, ws.topk_flat.view(64, 2), ws.gates_flat,
+                  ws.padded_slots, ws.block_expert_ids, ws.slot_to_row, ws.max_blocks,
+                  ws.max_blocks, ws.demand, ws.expert_offsets, ws.sorted_slots, ws.slot_pos,
+                  ws.tiles, ws.max_tiles)
+    bf = torch.bfloat16
+    x = torch.zeros(65, h, dtype=bf)
+    w1 = torch.zeros(e, i, h, dtype=bf)
+    w2 = torch.zeros(e, h, i, dtype=bf)
+    with pytest.raises(ValueError, match="different shape"):
+        m.tree_moe_forward(x, w1, w2, w1, torch.zeros(e, h, dtype=bf), torch.ones(65), 8,
+                           routing=r)

@@ -278,3 +278,51 @@ def test_tree_sampling_preserves_target_distribution():
         counts[int(toks[0]) if num else bonus] += 1
     sigma = np.sqrt(trials * p * (1 - p))
     assert np.all(np.abs(counts - trials * p) <= 6 * sigma)
+
+
+def _torch_softmax_argmax(x: torch.Tensor) -> int:
+    """The reference's pick: first-occurrence argmax of softmax in the row's
+    dtype (probs = empty_like(logits), op4_commit.py:211)."""
+    p = torch.softmax(x.float(), dim=-1).to(x.dtype).float().numpy()
+    return int(np.argmax(p))
+
+
+def test_softmax_argmax_planted_ties():
+    """Probabilities that round equal tie, and the first index wins although
+    its logit is smaller: fp32 (a 1e-9 gap at the maximum: e = 1 - 1e-9
+    rounds to 1) and bf16 (a one-ulp gap at 2^-8: the bf16 probabilities
+    round equal).  torch's softmax makes the same pick; the plain logit
+    argmax does not."""
+    from oracle import oracle_c
+
+    x = torch.full((1, 100), -10.0)
+    x[0, 5], x[0, 7] = 0.0, 1e-9
+    assert int(x.argmax()) == 7
+    assert oracle_c.softmax_argmax(x.numpy())[0] == 5 == _torch_softmax_argmax(x[0])
+    xb = torch.full((1, 64), -3.0, dtype=torch.bfloat16)
+    xb[0, 3] = 2.0 ** -8
+    xb[0, 9] = 2.0 ** -8 + 2.0 ** -15
+    assert float(xb[0, 9]) > float(xb[0, 3]) and int(xb.float().argmax()) == 9
+    got = oracle_c.softmax_argmax(bf16_bits(xb), bf16_bits=True)[0]
+    assert got == 3 == _torch_softmax_argmax(xb[0])
+    # without the bf16 rounding of the probabilities the pick would be 9
+    assert oracle_c.softmax_argmax(xb.float().numpy())[0] == 9
+    # a row of -inf: index 0
+    assert oracle_c.softmax_argmax(np.full((1, 8), -np.inf, np.float32))[0] == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_softmax_argmax_random_rows_agree_with_torch(dtype):
+    """On N(0, 3) rows (config-4 logits) the oracle's pick equals torch's
+    softmax pick (and here the logit argmax: no rounded ties at the top)."""
+    from oracle import oracle_c
+
+    g = torch.Generator().manual_seed(17)
+    x = (torch.randn(32, 32000, generator=g) * 3).to(dtype)
+    if dtype == torch.bfloat16:
+        got = oracle_c.softmax_argmax(bf16_bits(x), bf16_bits=True)
+    else:
+        got = oracle_c.softmax_argmax(x.numpy())
+    want = [_torch_softmax_argmax(x[r]) for r in range(32)]
+    assert got.tolist() == want
+    assert want == x.float().argmax(1).tolist()

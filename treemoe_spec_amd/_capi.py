@@ -28,12 +28,12 @@ SIGNATURES: dict[str, list] = {
     "tm_op1_combine": [P, P, P, I64, I64, I64, P],
     "tm_op1_prefill_gemm1": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P],
     "tm_op1_prefill_gemm2": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
-    "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, P, P, P, P, P, P],
+    "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, I64, I32, P, P, P, P, P, P],
     "tm_op4_kv_commit": [P, P, I64, I64, I64, I64, I64, I64, I64, P, P, P, I64, P, I64, I64,
                          I64, P],
     "tm_op4_rep_penalty": [P, I32, I64, I64, I64, P, I64, F32, P, I64, P],
-    "tm_op4_sample_walk": [P, I32, I64, I64, I64, P, I64, P, P, P, P, P, P, F32, P, P, P, P,
-                           P],
+    "tm_op4_sample_walk": [P, I32, I64, I64, I64, P, I64, P, P, P, P, I64, P, P, F32, P, P, P,
+                           P, P],
     "tm_tree_attention": [P, I64, P, P, I64, P, P, I64, I64, I64, P, I64, I64, P, I64, I32, P,
                           I64, I64, I64, I64, F32, P, I64, I64, P, I64, P],
     "tm_tree_attention_plan": [I64, I64, I64, I64, I64, I64, I64, P, P],

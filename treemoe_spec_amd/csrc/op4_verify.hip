@@ -124,6 +124,13 @@ tm_argmax_part_kernel(const void* __restrict__ logits, int V, int64_t row_stride
   }
 }
 
+// Entries of a node's child range [st, st + cnt) that lie inside the
+// num_edges-entry child list (all of them for a well-formed CSR).
+__device__ __forceinline__ int edge_count(int st, int cnt, int num_edges) {
+  if (st < 0 || st >= num_edges || cnt <= 0) return 0;
+  return min(cnt, num_edges - st);
+}
+
 struct WalkShared {
   int64_t tokens[kStageNodes];
   int argmax[kStageNodes];
@@ -146,20 +153,22 @@ __global__ void __launch_bounds__(kWalkThreads)
 tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
                const int64_t* __restrict__ tokens, const int32_t* __restrict__ child_start,
                const int32_t* __restrict__ child_count, const int32_t* __restrict__ child_list,
-               int max_depth, int32_t* __restrict__ argmax, int64_t* __restrict__ accepted_slots,
+               int num_edges, int max_depth, int32_t* __restrict__ argmax,
+               int64_t* __restrict__ accepted_slots,
                int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result) {
   __shared__ WalkShared sh;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const bool staged = N <= kStageNodes;
-  const int nlist = N > 1 ? N - 1 : 1;
+  // child_list holds num_edges entries; a node's range is clipped to it and a
+  // child index outside [0, N) never matches, so no read leaves the buffers.
+  const bool staged = N <= kStageNodes && num_edges <= kStageNodes;
   if (staged) {
     for (int i = tid; i < N; i += kWalkThreads) {
       sh.tokens[i] = tokens[i];
       sh.child_start[i] = child_start[i];
       sh.child_count[i] = child_count[i];
     }
-    for (int i = tid; i < nlist; i += kWalkThreads) sh.child_list[i] = child_list[i];
+    for (int i = tid; i < num_edges; i += kWalkThreads) sh.child_list[i] = child_list[i];
   }
   // Row partials: lane l of a wave takes part l % P of row r0 + l / P, with
   // P = parts rounded up to a power of two (<= 64), so one load per lane and
@@ -204,11 +213,11 @@ tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
     for (int i = tid; i < N; i += kWalkThreads) {
       const int64_t target = (int64_t)sh.argmax[i];
       const int st = sh.child_start[i];
-      const int cnt = sh.child_count[i];
+      const int cnt = edge_count(st, sh.child_count[i], num_edges);
       int acc = -1;
       for (int j = 0; j < cnt; ++j) {
         const int c = sh.child_list[st + j];
-        if (sh.tokens[c] == target) { acc = c; break; }
+        if (c >= 0 && c < N && sh.tokens[c] == target) { acc = c; break; }
       }
       sh.next[i] = acc;
     }
@@ -224,10 +233,10 @@ tm_walk_kernel(const Partial* __restrict__ partial, int parts, int N,
       } else {
         const int64_t target = (int64_t)am[node];
         const int st = cs[node];
-        const int cnt = cc[node];
+        const int cnt = edge_count(st, cc[node], num_edges);
         for (int j = 0; j < cnt; ++j) {
           const int c = cl[st + j];
-          if (tok[c] == target) { acc = c; break; }
+          if (c >= 0 && c < N && tok[c] == target) { acc = c; break; }
         }
       }
       if (acc < 0) break;
@@ -460,9 +469,9 @@ __device__ __forceinline__ void stage_tree(SampTree& s, int N, int V,
                                            const int32_t* __restrict__ child_start,
                                            const int32_t* __restrict__ child_count,
                                            const int32_t* __restrict__ child_list,
-                                           const float* __restrict__ uniforms,
+                                           int num_edges, const float* __restrict__ uniforms,
                                            const float* __restrict__ q, int64_t q_stride) {
-  const int nlist = N > 1 ? N - 1 : 1;
+  const int nlist = num_edges;
   for (int i = threadIdx.x; i < N; i += kSampThreads) {
     const int64_t t = tokens[i];
     const bool in = t >= 0 && t < V;
@@ -478,14 +487,13 @@ __device__ __forceinline__ void stage_tree(SampTree& s, int N, int V,
 
 // Child list entry `at` (staged or from global memory): the child's slot c
 // and its token (-1 outside [0, V)).
-__device__ __forceinline__ int2 sample_child(bool staged, const SampTree& s, int at, int V,
+// A child index outside [0, N) is returned as c = -1, which is never accepted.
+__device__ __forceinline__ int2 sample_child(bool staged, const SampTree& s, int at, int N, int V,
                                              const int64_t* __restrict__ tokens,
                                              const int32_t* __restrict__ child_list) {
-  if (staged) {
-    const int c = s.child_list[at];
-    return make_int2(c, s.tok[c]);
-  }
-  const int c = child_list[at];
+  const int c = staged ? s.child_list[at] : child_list[at];
+  if (c < 0 || c >= N) return make_int2(-1, -1);
+  if (staged) return make_int2(c, s.tok[c]);
   const int64_t t = tokens[c];
   return make_int2(c, (t >= 0 && t < V) ? (int)t : -1);
 }
@@ -653,7 +661,7 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
                           int vec_q, const int64_t* __restrict__ tokens,
                           const int32_t* __restrict__ child_start,
                           const int32_t* __restrict__ child_count,
-                          const int32_t* __restrict__ child_list,
+                          const int32_t* __restrict__ child_list, int num_edges,
                           const float* __restrict__ uniforms, const float* __restrict__ bonus_u,
                           float temperature, float* __restrict__ res, int vec_res,
                           int64_t* __restrict__ accepted_slots,
@@ -662,9 +670,10 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
   __shared__ SampTree tree;
   const int tid = threadIdx.x;
   const int lo = tid * R;
-  const bool staged = N <= kSampStage;
+  const bool staged = N <= kSampStage && num_edges <= kSampStage;
   if (staged)
-    stage_tree(tree, N, V, tokens, child_start, child_count, child_list, uniforms, q, q_stride);
+    stage_tree(tree, N, V, tokens, child_start, child_count, child_list, num_edges, uniforms, q,
+               q_stride);
   int phase = 0;
   const float rtemp = 1.0f / temperature;
   int node = 0;
@@ -694,11 +703,13 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
     for (int i = 0; i < R; ++i) r[i] = r[i] * rs;
 
     const int st = staged ? tree.child_start[node] : child_start[node];
-    const int cnt = staged ? tree.child_count[node] : child_count[node];
+    const int cnt = edge_count(st, staged ? tree.child_count[node] : child_count[node],
+                               num_edges);
     int taken = -1, taken_tok = -1;
     for (int j = 0; j < cnt; ++j) {
-      const int2 ct = sample_child(staged, tree, st + j, V, tokens, child_list);
+      const int2 ct = sample_child(staged, tree, st + j, N, V, tokens, child_list);
       const int c = ct.x, tok = ct.y;
+      if (c < 0) continue;
       // the owner of entry tok decides; tid 0 answers for an out-of-vocabulary token
       if (tok >= 0 ? tok / R == tid : tid == 0) {
         int ok = 0;
@@ -790,7 +801,7 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
                             int vec_q, const int64_t* __restrict__ tokens,
                             const int32_t* __restrict__ child_start,
                             const int32_t* __restrict__ child_count,
-                            const int32_t* __restrict__ child_list,
+                            const int32_t* __restrict__ child_list, int num_edges,
                             const float* __restrict__ uniforms, const float* __restrict__ bonus_u,
                             float temperature, float* __restrict__ res, int vec_res,
                             int64_t* __restrict__ accepted_slots,
@@ -802,9 +813,10 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
   const int tid = threadIdx.x;
   const int tiles = (V + kSampTile - 1) / kSampTile;
   const bool vl = vec_logits != 0, vq = vec_q != 0, vr = vec_res != 0;
-  const bool staged = N <= kSampStage;
+  const bool staged = N <= kSampStage && num_edges <= kSampStage;
   if (staged)
-    stage_tree(tree, N, V, tokens, child_start, child_count, child_list, uniforms, q, q_stride);
+    stage_tree(tree, N, V, tokens, child_start, child_count, child_list, num_edges, uniforms, q,
+               q_stride);
   const float rtemp = 1.0f / temperature;
   int phase = 0;
   int node = 0;
@@ -845,11 +857,13 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
     }
 
     const int st = staged ? tree.child_start[node] : child_start[node];
-    const int cnt = staged ? tree.child_count[node] : child_count[node];
+    const int cnt = edge_count(st, staged ? tree.child_count[node] : child_count[node],
+                               num_edges);
     int taken = -1, taken_tok = -1;
     for (int j = 0; j < cnt; ++j) {
-      const int2 ct = sample_child(staged, tree, st + j, V, tokens, child_list);
+      const int2 ct = sample_child(staged, tree, st + j, N, V, tokens, child_list);
       const int c = ct.x, tok = ct.y;
+      if (c < 0) continue;
       // the thread that wrote res[tok] decides; tid 0 for an out-of-vocabulary token
       if (tok >= 0 ? (tok % kSampTile) / kSampTR == tid : tid == 0) {
         int ok = 0;
@@ -958,10 +972,78 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
   }
 }
 
+// ---------------------------------------------------- softmax argmax --
+// Greedy verification with a repetition penalty takes the argmax of the
+// penalised rows' softmax, stored in the logits' dtype (reference
+// `_postprocess_softmax_kernel` at temperature 1, then `_argmax_kernel` over
+// the probabilities, op4_commit.py:207-214), not of the logits: values whose
+// rounded probabilities are equal tie, and the first index wins.  With
+// e_i = exp(x_i - max) and s = sum_i e_i, p_i = round(e_i / s) in fp32 (fp32
+// rows) or bf16 (bf16 rows).  exp is monotone and e = 1 at the maximum, so the
+// argmax is the first i with round(e_i / s) == round(1 / s).  One workgroup per
+// row: the maximum; the sum (thread-strided partials in index order, a xor
+// butterfly per wave, then the waves in order); the first matching index.  The
+// row's (round(1 / s), index) goes to partial[row] for tm_walk_kernel (one part
+// per row).  A row of -inf gives index 0.
+constexpr int kSmThreads = 256;
+
+template <int kDtype>
+__device__ __forceinline__ float round_prob(float p) {
+  if (kDtype == TM_DTYPE_F32) return p;
+  return tm_bf16_to_f32(tm_f32_to_bf16(p));
+}
+
+template <int kDtype>
+__global__ void __launch_bounds__(kSmThreads)
+tm_softmax_argmax_kernel(const void* __restrict__ logits, int V, int64_t row_stride,
+                         Partial* __restrict__ partial) {
+  __shared__ float s_red[kSmThreads / 64];
+  __shared__ int s_idx[kSmThreads / 64];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t base = (int64_t)row * row_stride;
+  float m = -INFINITY;
+  for (int i = tid; i < V; i += kSmThreads) m = fmaxf(m, logit_at<kDtype>(logits, base + i));
+  m = wave_max(m);
+  if (lane == 0) s_red[wave] = m;
+  __syncthreads();
+  m = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kSmThreads / 64; ++w) m = fmaxf(m, s_red[w]);
+  __syncthreads();
+  float s = 0.0f;
+  for (int i = tid; i < V; i += kSmThreads)
+    s = s + tm_expf_det(logit_at<kDtype>(logits, base + i) - m);
+  s = wave_sum(s);
+  if (lane == 0) s_red[wave] = s;
+  __syncthreads();
+  s = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kSmThreads / 64; ++w) s = s + s_red[w];
+  const float top = round_prob<kDtype>(1.0f / s);
+  int first = INT_MAX;
+  for (int i = tid; i < V; i += kSmThreads) {
+    if (round_prob<kDtype>(tm_expf_det(logit_at<kDtype>(logits, base + i) - m) / s) == top) {
+      first = i;
+      break;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) first = min(first, __shfl_xor(first, off));
+  if (lane == 0) s_idx[wave] = first;
+  __syncthreads();
+  if (tid == 0) {
+    int f = s_idx[0];
+#pragma unroll
+    for (int w = 1; w < kSmThreads / 64; ++w) f = min(f, s_idx[w]);
+    partial[row] = Partial{top, f == INT_MAX ? 0 : f};
+  }
+}
+
 template <int kDtype>
 void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, const float* q,
                         int64_t q_stride, const int64_t* tokens, const int32_t* child_start,
-                        const int32_t* child_count, const int32_t* child_list,
+                        const int32_t* child_count, const int32_t* child_list, int num_edges,
                         const float* uniforms, const float* bonus_u, float temperature,
                         float* res, int64_t* accepted_slots, int64_t* accepted_tokens,
                         int64_t* result, hipStream_t stream) {
@@ -972,7 +1054,7 @@ void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, co
 #define TM_SAMPLE_REG(R)                                                                       \
   hipLaunchKernelGGL((tm_sample_walk_reg_kernel<kDtype, R>), dim3(1), dim3(kSampThreads), 0,   \
                      stream, logits, N, V, row_stride, vl, q, q_stride, vq, tokens,           \
-                     child_start, child_count, child_list, uniforms, bonus_u, temperature, res, \
+                     child_start, child_count, child_list, num_edges, uniforms, bonus_u, temperature, res, \
                      vr, accepted_slots, accepted_tokens, result)
   if (V <= kSampThreads * 8) {
     TM_SAMPLE_REG(8);
@@ -984,7 +1066,7 @@ void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, co
   } else {
     hipLaunchKernelGGL(tm_sample_walk_tiled_kernel<kDtype>, dim3(1), dim3(kSampThreads), 0,
                        stream, logits, N, V, row_stride, vl, q, q_stride, vq, tokens,
-                       child_start, child_count, child_list, uniforms, bonus_u, temperature, res,
+                       child_start, child_count, child_list, num_edges, uniforms, bonus_u, temperature, res,
                        vr, accepted_slots, accepted_tokens, result);
   }
 #undef TM_SAMPLE_REG
@@ -995,14 +1077,35 @@ void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, co
 extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
                                   int64_t row_stride, const int64_t* tokens,
                                   const int32_t* child_start, const int32_t* child_count,
-                                  const int32_t* child_list, int64_t max_depth,
-                                  int32_t* argmax, int64_t* accepted_slots,
-                                  int64_t* accepted_tokens, int64_t* result, void* workspace,
-                                  void* stream) {
-  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || max_depth < 0)
+                                  const int32_t* child_list, int64_t num_edges,
+                                  int64_t max_depth, int softmax_argmax, int32_t* argmax,
+                                  int64_t* accepted_slots, int64_t* accepted_tokens,
+                                  int64_t* result, void* workspace, void* stream) {
+  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || max_depth < 0 ||
+      num_edges < 0 || num_edges > (1 << 24))
     return TM_ERR_SHAPE;
   if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
+  if (softmax_argmax != 0 && softmax_argmax != 1) return TM_ERR_ARG;
   if (((uintptr_t)workspace % 8) != 0) return TM_ERR_ALIGN;
+  Partial* partial = reinterpret_cast<Partial*>(workspace);
+  if (softmax_argmax) {
+    if (dtype == TM_DTYPE_F32) {
+      hipLaunchKernelGGL(tm_softmax_argmax_kernel<TM_DTYPE_F32>, dim3((unsigned)N),
+                         dim3(kSmThreads), 0, (hipStream_t)stream, logits, (int)V, row_stride,
+                         partial);
+    } else {
+      hipLaunchKernelGGL(tm_softmax_argmax_kernel<TM_DTYPE_BF16>, dim3((unsigned)N),
+                         dim3(kSmThreads), 0, (hipStream_t)stream, logits, (int)V, row_stride,
+                         partial);
+    }
+    TM_HIP_CHECK_LAUNCH();
+    hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, (hipStream_t)stream,
+                       partial, 1, (int)N, tokens, child_start, child_count, child_list,
+                       (int)num_edges, (int)max_depth, argmax, accepted_slots, accepted_tokens,
+                       result);
+    TM_HIP_CHECK_LAUNCH();
+    return TM_OK;
+  }
   const int64_t elem = (dtype == TM_DTYPE_F32) ? 4 : 2;
   const int64_t width = 16 / elem;  // elements per 16-byte vector
   // rows are split into `parts` ranges of `per_part` elements (a multiple of
@@ -1015,7 +1118,6 @@ extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int6
     parts = (V + per_part - 1) / per_part;
   }
   const int vec_ok = (((uintptr_t)logits % 16) == 0 && ((row_stride * elem) % 16) == 0) ? 1 : 0;
-  Partial* partial = reinterpret_cast<Partial*>(workspace);
   const dim3 grid((unsigned)parts, (unsigned)N);
   if (dtype == TM_DTYPE_F32) {
     hipLaunchKernelGGL(tm_argmax_part_kernel<TM_DTYPE_F32>, grid, dim3(kArgThreads), 0,
@@ -1029,7 +1131,8 @@ extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int6
   TM_HIP_CHECK_LAUNCH();
   hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, (hipStream_t)stream,
                      partial, (int)parts, (int)N, tokens, child_start, child_count, child_list,
-                     (int)max_depth, argmax, accepted_slots, accepted_tokens, result);
+                     (int)num_edges, (int)max_depth, argmax, accepted_slots, accepted_tokens,
+                     result);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
@@ -1074,22 +1177,23 @@ extern "C" int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int6
                                   int64_t row_stride, const float* draft_probs, int64_t q_stride,
                                   const int64_t* tokens, const int32_t* child_start,
                                   const int32_t* child_count, const int32_t* child_list,
-                                  const float* uniforms, const float* bonus_u,
+                                  int64_t num_edges, const float* uniforms, const float* bonus_u,
                                   float temperature, float* residual,
                                   int64_t* accepted_slots, int64_t* accepted_tokens,
                                   int64_t* result, void* stream) {
-  if (N < 1 || N > (1 << 20) || V < 1 || V > kSampMaxV || row_stride < V || q_stride < V)
+  if (N < 1 || N > (1 << 20) || V < 1 || V > kSampMaxV || row_stride < V || q_stride < V ||
+      num_edges < 0 || num_edges > (1 << 24))
     return TM_ERR_SHAPE;
   if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
   if (!(temperature > 0.0f)) return TM_ERR_ARG;
   if (dtype == TM_DTYPE_F32) {
     launch_sample_walk<TM_DTYPE_F32>(logits, (int)N, (int)V, row_stride, draft_probs, q_stride,
-                                     tokens, child_start, child_count, child_list, uniforms,
+                                     tokens, child_start, child_count, child_list, (int)num_edges, uniforms,
                                      bonus_u, temperature, residual, accepted_slots,
                                      accepted_tokens, result, (hipStream_t)stream);
   } else {
     launch_sample_walk<TM_DTYPE_BF16>(logits, (int)N, (int)V, row_stride, draft_probs, q_stride,
-                                      tokens, child_start, child_count, child_list, uniforms,
+                                      tokens, child_start, child_count, child_list, (int)num_edges, uniforms,
                                       bonus_u, temperature, residual, accepted_slots,
                                       accepted_tokens, result, (hipStream_t)stream);
   }

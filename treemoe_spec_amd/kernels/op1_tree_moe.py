@@ -384,8 +384,9 @@ def tree_moe_forward(
         routing = route_experts(x, router_weight, node_accept_prob, expert_budget, inter,
                                 routing_objective=routing_objective)
     ws = routing.ws
-    if (ws.h.shape != (ws.max_tiles * TILE_M, inter) or ws.partial.shape[2] != hidden
-            or routing.max_tiles > ws.max_tiles):
+    if (routing.topk_ids.shape[0] != n or ws.partial.shape[1] != 2 * n
+            or ws.h.shape != (ws.max_tiles * TILE_M, inter) or ws.partial.shape[2] != hidden
+            or ws.num_experts != e or routing.max_tiles > ws.max_tiles):
         raise ValueError("routing was computed for a different shape")
     stream = _capi.stream_of(x.device)
     split = ws.split

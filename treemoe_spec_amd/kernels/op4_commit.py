@@ -15,9 +15,9 @@ the host exactly like the reference (:267).
 
 Greedy with rep_penalty != 1 (reference :201-214) first penalises the logits
 in place (``tm_op4_rep_penalty``; without prev_tokens token 0 is penalised, as
-in the reference), then takes the argmax of the penalised logits.  The
-reference takes it over their rounded softmax, which can differ only where
-rounding makes two probabilities equal.
+in the reference), then, as the reference does, takes the first-occurrence
+argmax of their softmax rounded to the logits' dtype (equal rounded
+probabilities tie and the lower index wins).
 
 Sampling (temperature > 0) follows the reference's routing of that mode to
 ``tree_verify_ref`` (:187-196): the walk is unbounded (max_depth and
@@ -36,6 +36,7 @@ import torch
 
 from treemoe_spec_amd import _capi
 from treemoe_spec_amd._capi import TM_DTYPE_BF16, TM_DTYPE_F32, call, ptr
+from treemoe_spec_amd.kv_cache import device_tables_of, scratch_pages_of
 
 
 @dataclass
@@ -51,6 +52,31 @@ class VerifyResult:
 def argmax_workspace(n: int, device) -> torch.Tensor:
     """Scratch of the row-range argmax: N * TM_OP4_MAX_PARTS (value, index) pairs."""
     return torch.empty(n * _capi.TM_OP4_MAX_PARTS * 8, dtype=torch.uint8, device=device)
+
+
+class _Scratch:
+    """Per (N, device) internal buffers of the greedy path, reused by every
+    call on that device (stream-ordered, like the reference's workspaces):
+    the argmax row partials and the int32 argmax vector."""
+
+    __slots__ = ("partials", "argmax")
+
+    def __init__(self, n: int, device):
+        self.partials = argmax_workspace(n, device)
+        self.argmax = torch.empty(n, dtype=torch.int32, device=device)
+
+
+_scratch_cache: dict[tuple, _Scratch] = {}
+
+
+def _scratch(n: int, device) -> _Scratch:
+    key = (n, device)
+    ws = _scratch_cache.get(key)
+    if ws is None:
+        if len(_scratch_cache) > 16:
+            _scratch_cache.clear()
+        ws = _scratch_cache[key] = _Scratch(n, device)
+    return ws
 
 
 def _penalty_table_size(num_prev: int) -> int:
@@ -75,9 +101,8 @@ def _apply_rep_penalty(logits: torch.Tensor, dtype: int, prev_tokens, rep_penalt
          prev.numel(), float(rep_penalty), ptr(table), size, stream)
 
 
-def _children_csr(children: list[list[int]], n: int, device) -> torch.Tensor:
-    """[starts | counts | flat] int32 in one host->device copy, from pinned
-    memory and ordered on the current stream (no host synchronisation)."""
+def _pack_children(children: list[list[int]], n: int) -> tuple[list[int], int]:
+    """[starts | counts | flat] as one int32 list, and the number of edges."""
     if len(children) != n:
         raise ValueError(f"children must list {n} nodes, got {len(children)}")
     starts, counts, flat = [], [], []
@@ -87,11 +112,56 @@ def _children_csr(children: list[list[int]], n: int, device) -> torch.Tensor:
         flat.extend(kids)
     if flat and (min(flat) < 0 or max(flat) >= n):
         raise ValueError("child index out of range")
-    packed = starts + counts + (flat or [0])
+    return starts + counts + (flat or [0]), len(flat)
+
+
+def _children_csr(children: list[list[int]], n: int, device) -> tuple[torch.Tensor, int]:
+    """[starts | counts | flat] int32 on ``device`` and the edge count (the
+    length of ``flat``; trees padded with edge-free slots have fewer than
+    N - 1).  One host->device copy from pinned memory, ordered on the current
+    stream (no host synchronisation)."""
+    packed, num_edges = _pack_children(children, n)
     if torch.device(device).type != "cuda":
-        return torch.tensor(packed, dtype=torch.int32)
+        return torch.tensor(packed, dtype=torch.int32), num_edges
     host = torch.tensor(packed, dtype=torch.int32, pin_memory=True)
-    return host.to(device, non_blocking=True)
+    return host.to(device, non_blocking=True), num_edges
+
+
+# The child CSR is static metadata per tree shape (the reference flattens it
+# "once per tree shape", op4_commit.py:216): the device copy is kept per
+# (children list object, device) and reused while the list's contents are
+# unchanged, which one C-level list comparison checks.
+_csr_cache: dict[tuple, tuple[list, torch.Tensor, int]] = {}
+
+
+def _cached_csr(children: list[list[int]], n: int, device) -> tuple[torch.Tensor, int]:
+    key = (id(children), device)
+    hit = _csr_cache.get(key)
+    if hit is not None and hit[0] == children:
+        return hit[1], hit[2]
+    csr, num_edges = _children_csr(children, n, device)
+    if len(_csr_cache) > 64:
+        _csr_cache.clear()
+    _csr_cache[key] = ([list(k) for k in children], csr, num_edges)
+    return csr, num_edges
+
+
+def _commit(kv, res_slots: torch.Tensor, result: torch.Tensor, n: int, commit_depth: int,
+            dev, stream: int) -> None:
+    """Copy the KV rows of [root] + accepted path from the tree scratch to
+    positions seq_len, seq_len + 1, ... on the device; advance seq_len."""
+    tree_pages = scratch_pages_of(kv)
+    k, v = kv.k, kv.v
+    if not (k.is_contiguous() and v.is_contiguous() and v.shape == k.shape and k.dim() == 5):
+        raise ValueError("KV tensors must be contiguous [L, pages, page, kvh, hd] of equal shape")
+    if len(tree_pages) * kv.block_size < n:
+        raise ValueError("tree larger than the KV scratch pages")
+    kv._ensure_capacity(kv.seq_len + commit_depth + 1)   # reference :251
+    table, scratch = device_tables_of(kv, dev)
+    call("tm_op4_kv_commit", ptr(k), ptr(v), k.element_size(), k.shape[0],
+         k.shape[3] * k.shape[4], k.stride(0), k.stride(1), k.stride(2), kv.block_size,
+         ptr(res_slots), ptr(result), ptr(scratch), len(tree_pages), ptr(table),
+         len(kv.block_table), kv.seq_len, commit_depth, stream)
 
 
 def _tree_depth(children: list[list[int]]) -> int:
@@ -138,14 +208,19 @@ def fused_verify_commit(
         raise TypeError(f"target_logits must be float32 or bfloat16, got {target_logits.dtype}")
     n, v = target_logits.shape
     dev = target_logits.device
-    tokens = tree_tokens.to(device=dev, dtype=torch.int64).contiguous()
+    tokens = tree_tokens
+    if tokens.device != dev or tokens.dtype != torch.int64 or not tokens.is_contiguous():
+        tokens = tokens.to(device=dev, dtype=torch.int64).contiguous()
     if tokens.numel() != n:
         raise ValueError("tree_tokens must have one entry per node")
-    csr = _children_csr(children, n, dev)
-    slots = torch.empty(n, dtype=torch.int64, device=dev)
-    toks = torch.empty(n, dtype=torch.int64, device=dev)
-    result = torch.empty(3, dtype=torch.int64, device=dev)
+    csr, num_edges = _cached_csr(children, n, dev)
+    # fresh outputs every call (the reference returns new tensors): one
+    # allocation holding accepted_slots [N], accepted_tokens [N] and
+    # (bonus, num_accepted, next_root)
+    out = torch.empty(2 * n + 3, dtype=torch.int64, device=dev)
+    slots, toks, result = out[:n], out[n:2 * n], out[2 * n:]
     stream = _capi.stream_of(dev)
+    c_start, c_count, c_list = ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n
     if temperature != 0.0:
         q = draft_probs
         if (q is None or not q.is_cuda or q.dtype != torch.float32 or q.dim() != 2
@@ -156,34 +231,24 @@ def fused_verify_commit(
         bonus_u = torch.rand(1, generator=generator, device=dev)
         residual = torch.empty(v, dtype=torch.float32, device=dev)
         call("tm_op4_sample_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
-             ptr(q), q.stride(0), ptr(tokens), ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n,
+             ptr(q), q.stride(0), ptr(tokens), c_start, c_count, c_list, num_edges,
              ptr(uniforms), ptr(bonus_u), float(temperature), ptr(residual), ptr(slots),
              ptr(toks), ptr(result), stream)
         commit_depth = _tree_depth(children)
     else:
         if rep_penalty != 1.0:
             _apply_rep_penalty(target_logits, dtype, prev_tokens, rep_penalty, stream)
-        argmax = torch.empty(n, dtype=torch.int32, device=dev)
+        ws = _scratch(n, dev)
         call("tm_op4_argmax_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
-             ptr(tokens), ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n, max_depth, ptr(argmax),
-             ptr(slots), ptr(toks), ptr(result), ptr(argmax_workspace(n, dev)), stream)
+             ptr(tokens), c_start, c_count, c_list, num_edges, max_depth,
+             1 if rep_penalty != 1.0 else 0, ptr(ws.argmax),
+             ptr(slots), ptr(toks), ptr(result), ptr(ws.partials), stream)
         commit_depth = max_depth
     res = VerifyResult(accepted_slots=slots, accepted_tokens=toks,
                        bonus_token=result[0], num_accepted=result[1])
     if kv is not None:
         # commit [root] + accepted path: the root token's KV (tree slot 0) is
         # part of the committed sequence too (reference :242-247).
-        m_max = commit_depth + 1
-        kv._ensure_capacity(kv.seq_len + m_max)
-        table, scratch = kv.device_tables(dev)
-        k = kv.k
-        if not (k.is_contiguous() and kv.v.is_contiguous() and kv.v.shape == k.shape):
-            raise ValueError("KV tensors must be contiguous and of equal shape")
-        if len(kv.tree_pages) * kv.block_size < n:
-            raise ValueError("tree larger than the KV scratch pages")
-        call("tm_op4_kv_commit", ptr(k), ptr(kv.v), k.element_size(), k.shape[0],
-             k.shape[3] * k.shape[4], k.stride(0), k.stride(1), k.stride(2), kv.block_size,
-             ptr(slots), ptr(result), ptr(scratch), len(kv.tree_pages), ptr(table),
-             len(kv.block_table), kv.seq_len, commit_depth, stream)
-        kv.seq_len += int(res.num_accepted) + 1
+        _commit(kv, slots, result, n, commit_depth, dev, stream)
+        kv.seq_len += int(res.num_accepted) + 1   # the one D2H, reference :267
     return res

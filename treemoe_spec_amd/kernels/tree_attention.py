@@ -24,6 +24,7 @@ import torch
 
 from treemoe_spec_amd import _capi
 from treemoe_spec_amd._capi import call, ptr
+from treemoe_spec_amd.kv_cache import device_tables_of, scratch_pages_of
 
 _mask_cache: dict = {}
 
@@ -80,7 +81,10 @@ def tree_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv, layer:
     if scale is None:
         scale = hd ** -0.5
     bits = pack_tree_mask(tree_mask)
-    table, scratch = kv.device_tables(dev)
+    pages = scratch_pages_of(kv)
+    if write_tree and len(pages) * kv.block_size < n:
+        raise ValueError("tree larger than the KV scratch pages")
+    table, scratch = device_tables_of(kv, dev)
     seq_len = kv.seq_len
     chunks = ctypes.c_int64()
     wbytes = ctypes.c_int64()
@@ -95,7 +99,7 @@ def tree_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv, layer:
     vc = kv.v[layer]
     call("tm_tree_attention", ptr(q), q.stride(0), ptr(k), ptr(v), k.stride(0), ptr(kc),
          ptr(vc), kc.stride(0), kc.stride(1), kv.block_size, ptr(table),
-         max(1, len(kv.block_table)), seq_len, ptr(scratch), len(kv.tree_pages),
+         max(1, len(kv.block_table)), seq_len, ptr(scratch), len(pages),
          1 if write_tree else 0, ptr(bits), n, hq, kvh, hd, float(scale), ptr(out), hq * hd,
          chunk_keys, ptr(ws), wbytes.value, _capi.stream_of(dev))
     return out

@@ -79,6 +79,21 @@ class PagedKVCache:
     def slot_of(self, pos: int) -> tuple[int, int]:
         return self.block_table[pos // self.block_size], pos % self.block_size
 
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, start_pos: int) -> None:
+        """Write [T, kv_heads, head_dim] at positions start_pos .. start_pos+T-1
+        (prefill and autoregressive steps; reference kv_cache.py:62-78).  Page
+        and offset indices are computed on the host from block_table."""
+        t = k.shape[0]
+        self._ensure_capacity(start_pos + t)
+        bs = self.block_size
+        pos = range(start_pos, start_pos + t)
+        blks = torch.tensor([self.block_table[q // bs] for q in pos], device=self.k.device,
+                            dtype=torch.long)
+        offs = torch.tensor([q % bs for q in pos], device=self.k.device, dtype=torch.long)
+        self.k[layer, blks, offs] = k
+        self.v[layer, blks, offs] = v
+        self.seq_len = max(self.seq_len, start_pos + t)
+
     def write_tree(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """Write the KV rows of tree nodes 0..n-1 into the scratch pages."""
         n = k.shape[0]
@@ -91,6 +106,29 @@ class PagedKVCache:
                 break
             self.k[layer, page, : hi - lo] = k[lo:hi]
             self.v[layer, page, : hi - lo] = v[lo:hi]
+
+    def commit_tree(self, accepted_slots: torch.Tensor) -> None:
+        """Host-path commit (reference kv_cache.py:88-106): the valid (>= 0)
+        tree slots of ``accepted_slots``, in sequence order, are copied from
+        the scratch pages to positions seq_len, seq_len+1, ... of every layer,
+        and seq_len advances by their number.  Reads the count back to the
+        host, as the reference does; the device path is op4's kv commit."""
+        valid = accepted_slots[accepted_slots >= 0]
+        m = int(valid.numel())
+        if m == 0:
+            return
+        self._ensure_capacity(self.seq_len + m)
+        bs = self.block_size
+        dev = self.k.device
+        slots = valid.to(device=dev, dtype=torch.long)
+        pages = torch.tensor(self.tree_pages, device=dev, dtype=torch.long)
+        src_p, src_o = pages[slots // bs], slots % bs
+        dest = [self.slot_of(self.seq_len + j) for j in range(m)]
+        dst_p = torch.tensor([d[0] for d in dest], device=dev, dtype=torch.long)
+        dst_o = torch.tensor([d[1] for d in dest], device=dev, dtype=torch.long)
+        self.k[:, dst_p, dst_o] = self.k[:, src_p, src_o]
+        self.v[:, dst_p, dst_o] = self.v[:, src_p, src_o]
+        self.seq_len += m
 
     def device_tables(self, device) -> tuple[torch.Tensor, torch.Tensor]:
         """int32 copies of block_table and the scratch page list on ``device``,
@@ -116,3 +154,59 @@ class PagedKVCache:
         k = self.k[layer, idx].reshape(nblk * self.block_size, kvh, hd)[:t]
         v = self.v[layer, idx].reshape(nblk * self.block_size, kvh, hd)[:t]
         return k, v
+
+    def gather_with_tail(self, layer: int, k_tail: torch.Tensor,
+                         v_tail: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """Contiguous [seq_len + T, kv_heads, head_dim] K and V: the committed
+        prefix followed by the tree rows (reference kv_cache.py:125-145, the
+        input of the reference's SDPA tree attention; this build's tree
+        attention reads the pages in place instead)."""
+        s, t = self.seq_len, k_tail.shape[0]
+        bs = self.block_size
+        nblk = (s + bs - 1) // bs
+        idx = torch.tensor(self.block_table[:nblk], device=self.k.device, dtype=torch.long)
+        kvh, hd = self.k.shape[3], self.k.shape[4]
+        m = max(nblk * bs, s + t)
+        out_k = torch.empty(m, kvh, hd, device=self.k.device, dtype=self.k.dtype)
+        out_v = torch.empty_like(out_k)
+        if nblk:
+            torch.index_select(self.k[layer], 0, idx,
+                               out=out_k[:nblk * bs].view(nblk, bs, kvh, hd))
+            torch.index_select(self.v[layer], 0, idx,
+                               out=out_v[:nblk * bs].view(nblk, bs, kvh, hd))
+        out_k[s:s + t] = k_tail
+        out_v[s:s + t] = v_tail
+        return out_k[:s + t], out_v[:s + t]
+
+
+def scratch_pages_of(kv) -> list[int]:
+    """Tree scratch pages of a paged cache: ``tree_pages`` of this module's
+    cache, or the single ``tree_block`` of the reference's
+    (treemoe/model/kv_cache.py:41)."""
+    pages = getattr(kv, "tree_pages", None)
+    return list(pages) if pages is not None else [int(kv.tree_block)]
+
+
+# int32 device copies of the block table and scratch pages for caches without
+# ``device_tables`` (the reference's PagedKVCache), per cache object and
+# device, rebuilt when the host block table or scratch list changes.
+_table_cache: dict[tuple, tuple[list, list, torch.Tensor, torch.Tensor]] = {}
+
+
+def device_tables_of(kv, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """(block_table, scratch_pages) as int32 tensors on ``device`` for any
+    cache with the reference's attributes (block_table, tree_block or
+    tree_pages)."""
+    if hasattr(kv, "device_tables"):
+        return kv.device_tables(device)
+    pages = scratch_pages_of(kv)
+    key = (id(kv), torch.device(device))
+    hit = _table_cache.get(key)
+    if hit is not None and hit[0] == kv.block_table and hit[1] == pages:
+        return hit[2], hit[3]
+    table = torch.tensor(kv.block_table or [0], dtype=torch.int32, device=device)
+    scratch = torch.tensor(pages, dtype=torch.int32, device=device)
+    if len(_table_cache) > 16:
+        _table_cache.clear()
+    _table_cache[key] = (list(kv.block_table), pages, table, scratch)
+    return table, scratch
