@@ -612,7 +612,9 @@ def test_softmax_argmax_matches_oracle(dtype):
         else:
             want = oracle_c.softmax_argmax(x.numpy())
         if v > 100:
-            assert want[0] == 5 and want[1] == 3 and want[2] == 0
+            # row 0 ties in both dtypes; row 1 only once rounded to bf16
+            assert want[0] == 5 and want[2] == 0
+            assert want[1] == (3 if dtype == torch.bfloat16 else 9)
         xd = x.cuda()
         tokens = torch.zeros(n, dtype=torch.long, device="cuda")
         csr, edges = _children_csr([[] for _ in range(n)], n, "cuda")

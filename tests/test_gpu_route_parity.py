@@ -8,14 +8,27 @@ the host CPU (oracle/op1_ref.route_and_bucket), at the BASELINE configurations
 and 10 more seeds at the Mixtral T=64 shape.
 
 torch does not fix the fp32 summation order of a bf16 linear, so the device's
-bf16 logits may differ from torch's by one bf16 ulp where the fp32 sum lies
-next to a rounding boundary.  The test therefore requires:
-  * every device logit within one bf16 ulp of torch's (exact logits come from
-    the C oracle, which reproduces the device's gates bit for bit);
-  * topk_ids identical to torch's, except on rows explained by such a logit
-    difference: either the row itself has a differing logit, or the keep set
-    differs (then some logit differs and the keep order had a near-tie);
-  * renormalised gates within 1e-5 (relative) of torch's on identical rows.
+bf16 logits may differ from torch's where the two fp32 sums round to
+different bf16 values.  The test therefore requires:
+  * every device logit within the bound two fp32 summation orders allow:
+    |device - torch| <= 2 H 2^-24 sum_k |x_k w_k| + one bf16 ulp (the products
+    of bf16 values are exact in fp32; each order's sum is within
+    (H - 1) 2^-24 sum |x_k w_k| of the exact sum; rounding adds one ulp).
+    Exact device logits come from the C oracle, which reproduces the device's
+    gates bit for bit (asserted);
+  * topk_ids identical to torch's, except on rows explained by
+    - an exact tie: torch's gates at the two picks are equal in value at each
+      position, so the rows differ only in which of two exactly equal experts
+      is taken.  torch.topk orders exact ties in an implementation-defined
+      way (it varies with the host CPU); the device takes the lower expert id,
+      as the reference's own routing kernel does with its first-occurrence
+      argmax (op1_tree_moe.py:226-232);
+    - or a logit difference: the row itself has a differing logit, or the
+      keep set differs (then some logit differs and the keep order had a
+      near-tie);
+  * renormalised gates within 1e-5 (relative) of torch's on every row whose
+    logits are identical and whose ids are identical or differ only by an
+    exact tie (2e-2 where a logit differs by a bf16 ulp).
 The counts are printed (run with -s) and recorded in the design notes.
 """
 
@@ -91,15 +104,41 @@ def test_ids_match_torch_router(name, t, h, e, budget, seed, bias, objective, ac
                                   routing_objective=objective).tolist())
 
     differ = logits_d != logits_t
-    gap = (logits_d.float() - logits_t.float()).abs()
-    assert bool((gap <= _ulp(logits_t)).all()), "a device logit is more than one ulp off torch's"
+    gap = (logits_d.double() - logits_t.double()).abs()
+    absum = x.double().abs() @ router.double().abs().T
+    big = torch.maximum(logits_d.float().abs(), logits_t.float().abs())
+    bound = 2 * h * 2.0 ** -24 * absum + _ulp(big).double()
+    assert bool((gap <= bound).all()), "a device logit is off torch's by more than rounding"
+    ulps = gap / _ulp(big).double()
     rows = (ids_d != ids_t).any(1)
+    tie_rows, logit_rows = [], []
     for r in rows.nonzero().flatten().tolist():
+        gd = gates_t[r, ids_d[r]]
+        gt = gates_t[r, ids_t[r]]
+        if keep_d == keep_t and torch.equal(gd, gt):
+            # an exact tie: the device's pick is the lowest id among the tied
+            for k in range(2):
+                if int(ids_d[r, k]) != int(ids_t[r, k]):
+                    tied = [j for j in keep_d if gates_t[r, j] == gd[k]
+                            and j not in ids_d[r, :k].tolist()]
+                    assert int(ids_d[r, k]) == min(tied), (r, k, tied)
+            tie_rows.append(r)
+            continue
         assert keep_d != keep_t or bool(differ[r].any()), (
             f"row {r}: ids {ids_d[r].tolist()} vs torch {ids_t[r].tolist()} with identical "
-            "logits and keep set")
-    same = ~rows
+            "logits and keep set and unequal gates")
+        logit_rows.append(r)
+    # gates: tight where the row's logits are identical; where a logit differs
+    # by a bf16 ulp (2^-8 relative) the softmax moves by about as much
+    same = ~differ.any(1)
+    same[logit_rows] = False
     torch.testing.assert_close(w_d[same], w_t[same], rtol=1e-5, atol=1e-7)
-    print(f"  logits differing by one ulp: {int(differ.sum())} of {differ.numel()}; "
+    near = differ.any(1)
+    near[logit_rows] = False
+    torch.testing.assert_close(w_d[near], w_t[near], rtol=2e-2, atol=1e-4)
+    print(f"  logits differing from torch's: {int(differ.sum())} of {differ.numel()} "
+          f"(at most {float(ulps.max()):.0f} bf16 ulp); "
           f"keep set {'differs' if keep_d != keep_t else 'identical'}; "
-          f"rows with different ids: {int(rows.sum())} of {t}", flush=True)
+          f"rows with different ids: {int(rows.sum())} of {t} "
+          f"({len(tie_rows)} exact ties, {len(logit_rows)} from a logit difference)",
+          flush=True)
