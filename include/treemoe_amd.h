@@ -46,7 +46,9 @@ extern "C" {
 #define TM_GEMM_TILE_M 64      /* rows of one expert processed per GEMM tile */
 #define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
 
-/* ABI version (major*10000 + minor*100 + patch). */
+/* ABI version (major*10000 + minor*100 + patch): 2.0.0.  Version 2 added
+ * num_edges to tm_op4_argmax_walk / tm_op4_sample_walk and softmax_argmax to
+ * tm_op4_argmax_walk. */
 int tm_version(void);
 
 /* Human-readable text for a return code of any entry point. */

@@ -3,7 +3,7 @@
 
 #include "tm_common.h"
 
-extern "C" int tm_version(void) { return 100; }
+extern "C" int tm_version(void) { return 20000; }
 
 extern "C" const char* tm_status_string(int code) {
   switch (code) {
