@@ -45,6 +45,7 @@ extern "C" {
 #define TM_MAX_TOKENS 4096
 #define TM_GEMM_TILE_M 64      /* rows of one expert processed per GEMM tile */
 #define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
+#define TM_OP4_NOALLOC_MAX_NODES 2048  /* N limit of tm_op4_argmax_walk_noalloc */
 
 /* ABI version (major*10000 + minor*100 + patch): 2.0.0.  Version 2 added
  * num_edges to tm_op4_argmax_walk / tm_op4_sample_walk and softmax_argmax to
@@ -221,6 +222,27 @@ int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
                        int64_t* accepted_slots,
                        int64_t* accepted_tokens, int64_t* result,
                        void* workspace, void* stream);
+
+/*
+ * tm_op4_argmax_walk without the workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc): the row
+ * partials live in a static device array owned by the library, 1 MiB
+ * (TM_OP4_NOALLOC_MAX_NODES * TM_OP4_MAX_PARTS * 8 bytes) on every GPU the
+ * library runs on, held until the process ends.  N <= TM_OP4_NOALLOC_MAX_NODES
+ * (else TM_ERR_SHAPE).  Calls nothing that allocates.  All calls on one GPU
+ * share that array: calls that overlap on one GPU (other streams, other host
+ * threads) race and must be serialised by the caller.  Arguments, outputs and
+ * results as tm_op4_argmax_walk; `stream` must belong to a device this process
+ * can make current.
+ */
+int tm_op4_argmax_walk_noalloc(const void* logits, int dtype, int64_t N, int64_t V,
+                               int64_t row_stride, const int64_t* tokens,
+                               const int32_t* child_start, const int32_t* child_count,
+                               const int32_t* child_list, int64_t num_edges,
+                               int64_t max_depth, int softmax_argmax, int32_t* argmax,
+                               int64_t* accepted_slots, int64_t* accepted_tokens,
+                               int64_t* result, void* stream);
 
 /*
  * Repetition penalty, in place on every row of logits [N, V] (row stride

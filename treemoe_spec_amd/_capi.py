@@ -31,6 +31,8 @@ SIGNATURES: dict[str, list] = {
     "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, I64, I32, P, P, P, P, P, P],
     "tm_op4_kv_commit": [P, P, I64, I64, I64, I64, I64, I64, I64, P, P, P, I64, P, I64, I64,
                          I64, P],
+    "tm_op4_argmax_walk_noalloc": [P, I32, I64, I64, I64, P, P, P, P, I64, I64, I32, P, P, P,
+                                   P, P],
     "tm_op4_rep_penalty": [P, I32, I64, I64, I64, P, I64, F32, P, I64, P],
     "tm_op4_sample_walk": [P, I32, I64, I64, I64, P, I64, P, P, P, P, I64, P, P, F32, P, P, P,
                            P, P],
@@ -45,6 +47,7 @@ TM_DTYPE_F32 = 0
 TM_DTYPE_BF16 = 1
 TM_GEMM_TILE_M = 64
 TM_OP4_MAX_PARTS = 64
+TM_OP4_NOALLOC_MAX_NODES = 2048
 
 _lib = None
 

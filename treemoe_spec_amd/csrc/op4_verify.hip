@@ -1,7 +1,9 @@
 // op4 on gfx950: first-occurrence argmax over the vocabulary for every tree
 // node (row-chunked over many workgroups), the greedy accept walk from LDS in
 // one workgroup, and the paged KV commit of [root] + accepted path.
+#include <atomic>
 #include <climits>
+#include <mutex>
 
 #include "tm_common.h"
 
@@ -1074,35 +1076,28 @@ void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, co
 
 }  // namespace
 
-extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
-                                  int64_t row_stride, const int64_t* tokens,
-                                  const int32_t* child_start, const int32_t* child_count,
-                                  const int32_t* child_list, int64_t num_edges,
-                                  int64_t max_depth, int softmax_argmax, int32_t* argmax,
-                                  int64_t* accepted_slots, int64_t* accepted_tokens,
-                                  int64_t* result, void* workspace, void* stream) {
-  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || max_depth < 0 ||
-      num_edges < 0 || num_edges > (1 << 24))
-    return TM_ERR_SHAPE;
-  if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
-  if (softmax_argmax != 0 && softmax_argmax != 1) return TM_ERR_ARG;
-  if (((uintptr_t)workspace % 8) != 0) return TM_ERR_ALIGN;
-  Partial* partial = reinterpret_cast<Partial*>(workspace);
+namespace {
+
+// Shared by tm_op4_argmax_walk (caller's workspace) and
+// tm_op4_argmax_walk_noalloc (the library's static scratch).
+int argmax_walk(const void* logits, int dtype, int64_t N, int64_t V, int64_t row_stride,
+                const int64_t* tokens, const int32_t* child_start, const int32_t* child_count,
+                const int32_t* child_list, int64_t num_edges, int64_t max_depth,
+                int softmax_argmax, int32_t* argmax, int64_t* accepted_slots,
+                int64_t* accepted_tokens, int64_t* result, Partial* partial,
+                hipStream_t stream) {
   if (softmax_argmax) {
     if (dtype == TM_DTYPE_F32) {
       hipLaunchKernelGGL(tm_softmax_argmax_kernel<TM_DTYPE_F32>, dim3((unsigned)N),
-                         dim3(kSmThreads), 0, (hipStream_t)stream, logits, (int)V, row_stride,
-                         partial);
+                         dim3(kSmThreads), 0, stream, logits, (int)V, row_stride, partial);
     } else {
       hipLaunchKernelGGL(tm_softmax_argmax_kernel<TM_DTYPE_BF16>, dim3((unsigned)N),
-                         dim3(kSmThreads), 0, (hipStream_t)stream, logits, (int)V, row_stride,
-                         partial);
+                         dim3(kSmThreads), 0, stream, logits, (int)V, row_stride, partial);
     }
     TM_HIP_CHECK_LAUNCH();
-    hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, (hipStream_t)stream,
-                       partial, 1, (int)N, tokens, child_start, child_count, child_list,
-                       (int)num_edges, (int)max_depth, argmax, accepted_slots, accepted_tokens,
-                       result);
+    hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, stream, partial, 1,
+                       (int)N, tokens, child_start, child_count, child_list, (int)num_edges,
+                       (int)max_depth, argmax, accepted_slots, accepted_tokens, result);
     TM_HIP_CHECK_LAUNCH();
     return TM_OK;
   }
@@ -1120,21 +1115,120 @@ extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int6
   const int vec_ok = (((uintptr_t)logits % 16) == 0 && ((row_stride * elem) % 16) == 0) ? 1 : 0;
   const dim3 grid((unsigned)parts, (unsigned)N);
   if (dtype == TM_DTYPE_F32) {
-    hipLaunchKernelGGL(tm_argmax_part_kernel<TM_DTYPE_F32>, grid, dim3(kArgThreads), 0,
-                       (hipStream_t)stream, logits, (int)V, row_stride, (int)per_part,
-                       (int)parts, vec_ok, partial);
+    hipLaunchKernelGGL(tm_argmax_part_kernel<TM_DTYPE_F32>, grid, dim3(kArgThreads), 0, stream,
+                       logits, (int)V, row_stride, (int)per_part, (int)parts, vec_ok, partial);
   } else {
-    hipLaunchKernelGGL(tm_argmax_part_kernel<TM_DTYPE_BF16>, grid, dim3(kArgThreads), 0,
-                       (hipStream_t)stream, logits, (int)V, row_stride, (int)per_part,
-                       (int)parts, vec_ok, partial);
+    hipLaunchKernelGGL(tm_argmax_part_kernel<TM_DTYPE_BF16>, grid, dim3(kArgThreads), 0, stream,
+                       logits, (int)V, row_stride, (int)per_part, (int)parts, vec_ok, partial);
   }
   TM_HIP_CHECK_LAUNCH();
-  hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, (hipStream_t)stream,
-                     partial, (int)parts, (int)N, tokens, child_start, child_count, child_list,
+  hipLaunchKernelGGL(tm_walk_kernel, dim3(1), dim3(kWalkThreads), 0, stream, partial,
+                     (int)parts, (int)N, tokens, child_start, child_count, child_list,
                      (int)num_edges, (int)max_depth, argmax, accepted_slots, accepted_tokens,
                      result);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
+}
+
+int check_argmax_walk(int dtype, int64_t N, int64_t V, int64_t row_stride, int64_t num_edges,
+                      int64_t max_depth, int softmax_argmax) {
+  if (N < 1 || N > (1 << 20) || V < 1 || V > (1 << 30) || row_stride < V || max_depth < 0 ||
+      num_edges < 0 || num_edges > (1 << 24))
+    return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_F32 && dtype != TM_DTYPE_BF16) return TM_ERR_ARG;
+  if (softmax_argmax != 0 && softmax_argmax != 1) return TM_ERR_ARG;
+  return TM_OK;
+}
+
+}  // namespace
+
+extern "C" int tm_op4_argmax_walk(const void* logits, int dtype, int64_t N, int64_t V,
+                                  int64_t row_stride, const int64_t* tokens,
+                                  const int32_t* child_start, const int32_t* child_count,
+                                  const int32_t* child_list, int64_t num_edges,
+                                  int64_t max_depth, int softmax_argmax, int32_t* argmax,
+                                  int64_t* accepted_slots, int64_t* accepted_tokens,
+                                  int64_t* result, void* workspace, void* stream) {
+  const int rc = check_argmax_walk(dtype, N, V, row_stride, num_edges, max_depth, softmax_argmax);
+  if (rc) return rc;
+  if (((uintptr_t)workspace % 8) != 0) return TM_ERR_ALIGN;
+  return argmax_walk(logits, dtype, N, V, row_stride, tokens, child_start, child_count,
+                     child_list, num_edges, max_depth, softmax_argmax, argmax, accepted_slots,
+                     accepted_tokens, result, reinterpret_cast<Partial*>(workspace),
+                     (hipStream_t)stream);
+}
+
+// ------------------------------------------------- allocation-free variant --
+// tm_op4_argmax_walk_noalloc keeps its row-range partials in this array
+// instead of a caller's workspace: 1 MiB of device memory that every GPU the
+// library runs on holds until the process ends (each device has its own copy).
+// In host code the name is not a device address; the address of a device's
+// copy comes from hipGetSymbolAddress, taken once per device (with that device
+// current) on its first call and kept in g_scratch_addr.
+static __device__ __align__(256) Partial scratch[TM_OP4_NOALLOC_MAX_NODES * TM_OP4_MAX_PARTS];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+std::atomic<Partial*> g_scratch_addr[kMaxDevices];
+
+// Device address of `scratch` on the device that runs `stream` (the current
+// device for the null stream).
+int scratch_address(hipStream_t stream, Partial** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return TM_ERR_HIP_BASE + (int)e;
+  int dev = cur;
+  if (stream != nullptr) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) return TM_ERR_HIP_BASE + (int)e;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return TM_ERR_ARG;
+  Partial* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) {
+    *out = p;
+    return TM_OK;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+  if (p == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return TM_ERR_HIP_BASE + (int)e;
+    void* addr = nullptr;
+    e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    const hipError_t back = dev != cur ? hipSetDevice(cur) : hipSuccess;
+    if (e != hipSuccess) return TM_ERR_HIP_BASE + (int)e;
+    if (back != hipSuccess) return TM_ERR_HIP_BASE + (int)back;
+    if (addr == nullptr) return TM_ERR_HIP_BASE + (int)hipErrorInvalidSymbol;
+    p = static_cast<Partial*>(addr);
+    g_scratch_addr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return TM_OK;
+}
+
+}  // namespace
+
+extern "C" int tm_op4_argmax_walk_noalloc(const void* logits, int dtype, int64_t N, int64_t V,
+                                          int64_t row_stride, const int64_t* tokens,
+                                          const int32_t* child_start,
+                                          const int32_t* child_count,
+                                          const int32_t* child_list, int64_t num_edges,
+                                          int64_t max_depth, int softmax_argmax,
+                                          int32_t* argmax, int64_t* accepted_slots,
+                                          int64_t* accepted_tokens, int64_t* result,
+                                          void* stream) {
+  const int rc = check_argmax_walk(dtype, N, V, row_stride, num_edges, max_depth, softmax_argmax);
+  if (rc) return rc;
+  if (N > TM_OP4_NOALLOC_MAX_NODES) return TM_ERR_SHAPE;
+  Partial* partial = nullptr;
+  const int src = scratch_address((hipStream_t)stream, &partial);
+  if (src) return src;
+  // every partial the walk reads is written by this call's first launch, so
+  // the array needs no clearing
+  return argmax_walk(logits, dtype, N, V, row_stride, tokens, child_start, child_count,
+                     child_list, num_edges, max_depth, softmax_argmax, argmax, accepted_slots,
+                     accepted_tokens, result, partial, (hipStream_t)stream);
 }
 
 extern "C" int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V,
