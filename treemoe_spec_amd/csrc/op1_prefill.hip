@@ -32,6 +32,8 @@
 // walked in super-blocks of 8 M-tiles x 4 columns (job_of).
 #pragma clang fp contract(off)
 
+#include <algorithm>
+
 #include "tm_common.h"
 
 namespace {
@@ -101,27 +103,52 @@ constexpr int kXcds = 8;  // workgroup i runs on XCD i % 8
 constexpr int SBM = 8;    // super-block: M-tile slots (consecutive: mostly one expert) ..
 constexpr int SBN = 4;    // .. x column jobs, M fastest
 
-// Job of launch index L: M-tile slot and column job (either may be padding,
-// which the kernels skip).  XCD x = L % 8 owns the column jobs
-// [x * cpx, (x + 1) * cpx) for every M-tile slot, so each weight block is read
-// through one XCD's L2 only, and walks them in SBM x SBN super-blocks: the
-// ~32 workgroups resident on the XCD share each A tile across SBN columns and
-// each weight block across the M-tiles of one expert.
-__device__ __forceinline__ void job_of(int L, int mt_max, int ncol, int* mt, int* col) {
-  const int x = L % kXcds, l = L / kXcds;
-  const int cpx = (ncol + kXcds - 1) / kXcds;
-  const int nsm = (mt_max + SBM - 1) / SBM;
-  const int sb = l / (SBM * SBN), w = l - sb * (SBM * SBN);
-  const int sbm = sb % nsm, sbn = sb / nsm;
-  *mt = sbm * SBM + w % SBM;
-  const int lc = sbn * SBN + w / SBM;  // column within the XCD's range
-  *col = lc < cpx ? x * cpx + lc : ncol;
+// Real M-tiles of this layer: sum over experts of ceil(rows_e / BM), from the
+// compact offsets (computed by every workgroup; E <= 64 loads).
+template <class C>
+__device__ __forceinline__ int count_mtiles(const int32_t* __restrict__ offsets, int E) {
+  __shared__ int s_n;
+  if (threadIdx.x < 64) {
+    int n = 0;
+    if ((int)threadIdx.x < E) {
+      const int cnt = offsets[threadIdx.x + 1] - offsets[threadIdx.x];
+      n = (cnt + C::PBM - 1) / C::PBM;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) n += __shfl_xor(n, o);
+    if (threadIdx.x == 0) s_n = n;
+  }
+  __syncthreads();
+  return s_n;
 }
 
-// Launch size: 8 XCDs x every (M-tile slot, column) pair of one XCD's range.
+// Job of launch index L over the layer's real M-tiles (n_mt of them): M-tile
+// and column job, or false for a launch index past the real jobs (those are
+// the launch's last indices, so the real jobs all start in the first round).
+// XCD x = L % 8 owns the column jobs [x * cpx, (x + 1) * cpx) for every
+// M-tile, so each weight block is read through one XCD's L2 only, and walks
+// them in strips of SBN columns, each strip in groups of SBM M-tiles, M
+// fastest (the last strip and group may be narrower): the ~32 workgroups
+// resident on the XCD share each A tile across SBN columns and each weight
+// block across the M-tiles of one expert.
+__device__ __forceinline__ bool job_of(int L, int n_mt, int ncol, int* mt, int* col) {
+  const int x = L % kXcds, l = L / kXcds;
+  const int cpx = (ncol + kXcds - 1) / kXcds;
+  if (l >= n_mt * cpx) return false;
+  const int s = l / (n_mt * SBN);                // column strip
+  const int ws = min(SBN, cpx - s * SBN);         // its width
+  const int j = l - s * n_mt * SBN;
+  const int g = j / (SBM * ws);                  // M-tile group within the strip
+  const int mg = min(SBM, n_mt - g * SBM);       // its size
+  const int jj = j - g * SBM * ws;
+  *mt = g * SBM + jj % mg;
+  *col = x * cpx + s * SBN + jj / mg;
+  return *col < ncol;
+}
+
+// Launch size: 8 XCDs x (M-tile bound) x the columns of one XCD's range.
 int64_t launch_jobs(int64_t mt_max, int64_t ncol) {
-  const int64_t cpx = (ncol + kXcds - 1) / kXcds;
-  return kXcds * ((mt_max + SBM - 1) / SBM) * ((cpx + SBN - 1) / SBN) * SBM * SBN;
+  return kXcds * mt_max * ((ncol + kXcds - 1) / kXcds);
 }
 
 // M-tile `idx` of the compact expert-major order: expert, first row, rows.
@@ -349,9 +376,9 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   const Stages sb{s0, s1, s2, s3};
   int mt, cb;
   const int ncol = I / (PBN / 2);
-  job_of((int)blockIdx.x, mt_max, ncol, &mt, &cb);
+  const int n_mt = min(count_mtiles<C>(offsets, E), mt_max);
+  if (!job_of((int)blockIdx.x, n_mt, ncol, &mt, &cb)) return;
   int e, p0, rows;
-  if (mt >= mt_max || cb >= ncol) return;
   if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows)) return;
   const int n0 = cb * (PBN / 2);  // first h column of the block
 
@@ -436,8 +463,8 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   __shared__ __attribute__((aligned(16))) uint8_t s3[C::NSTAGE > 3 ? C::STAGE : 16];
   int mt, job;  // job = (column block, segment)
   const int ncol = (H / PBN) * nsplit;
-  job_of((int)blockIdx.x, mt_max, ncol, &mt, &job);
-  if (mt >= mt_max || job >= ncol) return;
+  const int n_mt = min(count_mtiles<C>(offsets, E), mt_max);
+  if (!job_of((int)blockIdx.x, n_mt, ncol, &mt, &job)) return;
   const int cb = job / nsplit;
   const int seg = job - cb * nsplit;
   int e, p0, rows;
@@ -501,7 +528,8 @@ extern "C" int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w
   // operand bytes per flop, but below that their coarser jobs and padding
   // cost more than that saves (measured at the Mixtral shape)
   const bool big = 2 * T >= 384 * E;
-  const int64_t mt_max = big ? mtile_bound<Tile256>(2 * T, E) : mtile_bound<Tile128>(2 * T, E);
+  const int64_t mt_max = std::min<int64_t>(
+      max_tiles, big ? mtile_bound<Tile256>(2 * T, E) : mtile_bound<Tile128>(2 * T, E));
   const int64_t jobs = launch_jobs(mt_max, I / (PBN / 2));
   if (jobs > INT32_MAX) return TM_ERR_SHAPE;
   if (big) {
@@ -528,7 +556,7 @@ extern "C" int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y,
   if (klen < C::PBK || (klen % C::PBK) != 0 || H < PBN || (H % PBN) != 0) return TM_ERR_SHAPE;
   if (H * I * 2 >= (int64_t)kOOR || 2 * T * I * 2 >= (int64_t)kOOR) return TM_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w2) || !aligned16(y)) return TM_ERR_ALIGN;
-  const int64_t mt_max = mtile_bound<C>(2 * T, E);
+  const int64_t mt_max = std::min<int64_t>(max_tiles, mtile_bound<C>(2 * T, E));
   const int64_t jobs = launch_jobs(mt_max, (H / PBN) * split);
   if (jobs > INT32_MAX) return TM_ERR_SHAPE;
   hipLaunchKernelGGL(tm_prefill_gemm2_kernel<C>, dim3((unsigned)jobs), dim3(NT), 0,
