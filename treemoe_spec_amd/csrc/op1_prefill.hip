@@ -402,7 +402,7 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   }
   // a tile with at most BM / 2 real rows (an expert's last) runs half the
   // MFMAs; its A rows past `rows` are loaded as zeros without memory traffic
-  if constexpr (C::MT > 2) {
+  if constexpr (C::MT > 1) {
     if (rows <= C::PBM / 2) {
       gemm1_tile<C, C::MT / 2>(sb, d, H / C::PBK, rows, p0, n0, I, h);
       return;
@@ -489,7 +489,7 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   }
   const Stages sb{s0, s1, s2, s3};
   float* ys = y + (size_t)seg * R * H + n0;
-  if constexpr (C::MT > 2) {
+  if constexpr (C::MT > 1) {
     if (rows <= C::PBM / 2) {  // as in gate/up
       gemm2_tile<C, C::MT / 2>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots, ys);
       return;
