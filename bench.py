@@ -366,7 +366,7 @@ def secondary(m, inp2, args) -> dict:
         _capi.call("tm_op4_kv_commit", k.data_ptr(), kv.v.data_ptr(), k.element_size(),
                    k.shape[0], k.shape[3] * k.shape[4], k.stride(0), k.stride(1), k.stride(2),
                    kv.block_size, slots.data_ptr(), result.data_ptr(), scratch.data_ptr(),
-                   len(kv.tree_pages), table.data_ptr(), len(kv.block_table), 4096, 8, stream)
+                   len(kv.tree_pages), table.data_ptr(), len(kv.block_table), 4096, 8, 0, stream)
 
     for _ in range(3):
         device_step()

@@ -47,13 +47,18 @@ extern "C" {
 #define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
 #define TM_OP4_NOALLOC_MAX_NODES 2048  /* N limit of tm_op4_argmax_walk_noalloc */
 
-/* ABI version (major*10000 + minor*100 + patch): 2.0.0.  Version 2 added
+/* ABI version (major*10000 + minor*100 + patch): 3.0.0.  Version 2 added
  * num_edges to tm_op4_argmax_walk / tm_op4_sample_walk and softmax_argmax to
- * tm_op4_argmax_walk. */
+ * tm_op4_argmax_walk; version 3 added host_count to tm_op4_kv_commit. */
 int tm_version(void);
 
 /* Human-readable text for a return code of any entry point. */
 const char* tm_status_string(int code);
+
+/* Device address of pinned host memory (hipHostGetDevicePointer), for
+ * arguments the kernels write to host memory (tm_op4_kv_commit's host_count).
+ * No reference counterpart: a utility of this ABI. */
+int tm_host_device_pointer(void* host, void** device);
 
 /* ---------------------------------------------------------------- op1 -- */
 
@@ -297,6 +302,10 @@ int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int64_t V, int6
  *   k[l, dst] = k[l, src] and v[l, dst] = v[l, src], row_bytes bytes each.
  * k, v: [L, pages, page_size, kvh, hd] with strides (elements of elem_bytes):
  * stride_layer, stride_page, stride_slot.  Grid covers j <= max_depth.
+ * host_count: NULL, or the device address (tm_host_device_pointer) of a pinned
+ * host int64 that receives num_accepted with a system-scope store early in the
+ * launch; the caller can then read the count without a device-to-host copy
+ * (the reference reads it with .item(), op4_commit.py:267).
  */
 int tm_op4_kv_commit(void* k, void* v, int64_t elem_bytes, int64_t L,
                      int64_t row_elems, int64_t stride_layer,
@@ -305,7 +314,7 @@ int tm_op4_kv_commit(void* k, void* v, int64_t elem_bytes, int64_t L,
                      const int64_t* result, const int32_t* scratch_pages,
                      int64_t num_scratch_pages, const int32_t* block_table,
                      int64_t num_table_pages, int64_t seq_len,
-                     int64_t max_depth, void* stream);
+                     int64_t max_depth, int64_t* host_count, void* stream);
 
 /*
  * Tree attention: the verification forward's attention over the paged KV

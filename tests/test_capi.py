@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
     assert set(_capi.SIGNATURES) <= set(declared_functions())
-    assert lib.tm_version() == 20000
+    assert lib.tm_version() == 30000
 
 
 def test_status_strings():
@@ -174,3 +174,15 @@ def test_route_bucket_argument_errors():
     args = list(base)
     args[8] = 4096       # padded rows beyond the workgroup's table
     assert fn(*args) == 1001
+
+
+def test_cpython_binding_loads_and_checks_arguments():
+    """The CPython binding of the per-step op4 calls is built and rejects a
+    wrong argument count before calling into the library."""
+    import pytest
+
+    from treemoe_spec_amd import _tmfast
+
+    for name in ("argmax_walk", "kv_commit"):
+        with pytest.raises(TypeError):
+            getattr(_tmfast, name)(1, 2, 3)

@@ -99,7 +99,7 @@ def test_kv_commit_on_fixture(op4g):
     _capi.call("tm_op4_kv_commit", k.data_ptr(), v.data_ptr(), 2, k.shape[0],
                k.shape[3] * k.shape[4], k.stride(0), k.stride(1), k.stride(2), k.shape[2],
                acc.data_ptr(), result.data_ptr(), scratch.data_ptr(), scratch.numel(),
-               table.data_ptr(), table.numel(), int(op4g["kv/seq_len"]), 8,
+               table.data_ptr(), table.numel(), int(op4g["kv/seq_len"]), 8, 0,
                _capi.stream_of(k.device))
     torch.cuda.synchronize()
     assert np.array_equal(k.cpu().view(torch.int16).numpy().view(np.uint16), op4g["kv/k_after"])

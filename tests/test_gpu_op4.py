@@ -223,6 +223,42 @@ def test_kv_commit_bytes(page, layers, kvh, hd, seq_len, dtype):
     assert torch.equal(res.accepted_slots.cpu(), ref_slots)
 
 
+@pytest.mark.parametrize("binding", ["cpython", "ctypes"])
+def test_commit_count_word_across_calls(monkeypatch, binding):
+    """num_accepted reaches the host through the pinned word the KV commit
+    writes: back-to-back calls with different accepted paths each read their
+    own count, and the synchronising fallback (no spin) reads the same.  Both
+    bindings of the C ABI (the CPython module and ctypes) are exercised."""
+    _say(f"kv commit count word, 6 calls, {binding} binding")
+    op4 = _op4()
+    if binding == "ctypes":
+        monkeypatch.setattr(op4, "_fast", None)
+    else:
+        assert op4._fast is not None, "the CPython binding is not built"
+    from treemoe_spec_amd.workloads import op4_workload
+
+    n, seq0 = 64, 100
+    kv = _kv_setup(2, 2, 16, 16, 80, seq0, n, 5, torch.bfloat16)
+    ws = op4._scratch(n, torch.device("cuda", torch.cuda.current_device()))
+    nums = []
+    for call, seed in enumerate((11, 12, 13, 14, 15, 16)):
+        if call == 3:
+            monkeypatch.setattr(op4, "_NOTE_SPIN_S", 0.0)
+        w = op4_workload(n=n, vocab=4096, max_depth=8, seed=seed)
+        _, _, _, ref_num = op4_ref.tree_verify(w.logits.float(), None, w.tokens, w.children)
+        before = kv.seq_len
+        res = op4.fused_verify_commit(w.logits.cuda(), None, w.tokens.cuda(), w.parent.cuda(),
+                                      w.children, kv=kv, max_depth=8)
+        assert kv.seq_len == before + ref_num + 1, (call, seed)
+        torch.cuda.synchronize()
+        assert int(res.num_accepted) == ref_num
+        key = next(k for k in op4._scratch_cache if k[0] == n)
+        ws = op4._scratch_cache[key]
+        assert ws.note_dev != 0 and int(ws.note_np[0]) == ref_num
+        nums.append(ref_num)
+    assert len(set(nums)) > 1, "the seeds should give different path lengths"
+
+
 def test_config4_planted_path_accepted():
     _say("config4 planted path")
     op4 = _op4()

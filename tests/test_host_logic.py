@@ -278,6 +278,7 @@ def test_op4_commit_host_logic_with_reference_cache(monkeypatch):
         seen["name"], seen["args"] = name, args
 
     monkeypatch.setattr(op4_commit, "call", fake_call)
+    monkeypatch.setattr(op4_commit, "_fast", None)
     slots = torch.tensor([3, 9, 30] + [-1] * 61)
     result = torch.tensor([7, 3, 30])
     op4_commit._commit(kv, slots, result, 64, 6, torch.device("cpu"), 0)

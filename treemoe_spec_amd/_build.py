@@ -81,9 +81,26 @@ def build_oracle() -> Path:
     return ORACLE_LIB
 
 
+def build_fast_binding() -> Path:
+    """_tmfast: CPython-API calls of the per-step op4 entry points, linked
+    against libtreemoe_amd.so in the same directory."""
+    import sysconfig
+
+    suffix = sysconfig.get_config_var("EXT_SUFFIX") or ".so"
+    out = PKG / ("_tmfast" + suffix)
+    tmp = out.with_suffix(".tmp")
+    cxx = os.environ.get("CXX", "g++")
+    _run([cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall",
+          f"-I{sysconfig.get_paths()['include']}", "-o", str(tmp), str(CSRC / "pyfast.cpp"),
+          f"-L{PKG}", "-ltreemoe_amd", "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
+
+
 def build_all() -> None:
     build_oracle()
     build_library()
+    build_fast_binding()
 
 
 if __name__ == "__main__":

@@ -30,7 +30,8 @@ SIGNATURES: dict[str, list] = {
     "tm_op1_prefill_gemm2": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
     "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, I64, I32, P, P, P, P, P, P],
     "tm_op4_kv_commit": [P, P, I64, I64, I64, I64, I64, I64, I64, P, P, P, I64, P, I64, I64,
-                         I64, P],
+                         I64, P, P],
+    "tm_host_device_pointer": [P, P],
     "tm_op4_argmax_walk_noalloc": [P, I32, I64, I64, I64, P, P, P, P, I64, I64, I32, P, P, P,
                                    P, P],
     "tm_op4_rep_penalty": [P, I32, I64, I64, I64, P, I64, F32, P, I64, P],
@@ -88,6 +89,14 @@ def ptr(t) -> int:
 
 
 def stream_of(device) -> int:
+    """Raw handle of torch's current stream on ``device`` (a torch.device,
+    'cuda[:N]' or an index)."""
     import torch
 
-    return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(device, int):
+        idx = device
+    else:
+        idx = (device if isinstance(device, torch.device) else torch.device(device)).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)

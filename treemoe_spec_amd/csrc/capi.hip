@@ -3,7 +3,13 @@
 
 #include "tm_common.h"
 
-extern "C" int tm_version(void) { return 20000; }
+extern "C" int tm_version(void) { return 30000; }
+
+extern "C" int tm_host_device_pointer(void* host, void** device) {
+  if (host == nullptr || device == nullptr) return TM_ERR_ARG;
+  const hipError_t e = hipHostGetDevicePointer(device, host, 0);
+  return e == hipSuccess ? TM_OK : TM_ERR_HIP_BASE + (int)e;
+}
 
 extern "C" const char* tm_status_string(int code) {
   switch (code) {

@@ -267,10 +267,16 @@ tm_kv_commit_kernel(uint8_t* __restrict__ k, uint8_t* __restrict__ v, int64_t ro
                     int64_t page_size, const int64_t* __restrict__ accepted_slots,
                     const int64_t* __restrict__ result, const int32_t* __restrict__ scratch_pages,
                     int64_t n_scratch, const int32_t* __restrict__ block_table, int64_t n_table,
-                    int64_t seq_len, int vec16) {
+                    int64_t seq_len, int vec16, int64_t* __restrict__ host_count) {
   const int layer = blockIdx.x;
   const int j = blockIdx.y;
   const int64_t num = result[1];
+  // the accepted count for the host: a system-scope store to its mapped word,
+  // pushed out of the GPU caches at once, so the host reads it without a copy
+  if (host_count != nullptr && layer == 0 && j == 0 && threadIdx.x == 0) {
+    __hip_atomic_store(host_count, num, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "");
+  }
   if (j > num) return;
   const int64_t s = (j == 0) ? 0 : accepted_slots[j - 1];
   if (s < 0 || s / page_size >= n_scratch) return;
@@ -1301,7 +1307,8 @@ extern "C" int tm_op4_kv_commit(void* k, void* v, int64_t elem_bytes, int64_t L,
                                 const int64_t* accepted_slots, const int64_t* result,
                                 const int32_t* scratch_pages, int64_t num_scratch_pages,
                                 const int32_t* block_table, int64_t num_table_pages,
-                                int64_t seq_len, int64_t max_depth, void* stream) {
+                                int64_t seq_len, int64_t max_depth, int64_t* host_count,
+                                void* stream) {
   if (L < 1 || L > 65535 || row_elems < 1 || page_size < 1 || max_depth < 0 ||
       max_depth > 65534 || num_scratch_pages < 1 || num_table_pages < 1 || seq_len < 0)
     return TM_ERR_SHAPE;
@@ -1318,7 +1325,7 @@ extern "C" int tm_op4_kv_commit(void* k, void* v, int64_t elem_bytes, int64_t L,
   hipLaunchKernelGGL(tm_kv_commit_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      (uint8_t*)k, (uint8_t*)v, row_bytes, sl, sp, ss, page_size,
                      accepted_slots, result, scratch_pages, num_scratch_pages, block_table,
-                     num_table_pages, seq_len, vec16);
+                     num_table_pages, seq_len, vec16, host_count);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }

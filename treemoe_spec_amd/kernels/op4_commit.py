@@ -30,13 +30,23 @@ the random stream).  One launch, ``tm_op4_sample_walk``.
 
 from __future__ import annotations
 
+import ctypes
+import time
 from dataclasses import dataclass
 
 import torch
 
 from treemoe_spec_amd import _capi
-from treemoe_spec_amd._capi import TM_DTYPE_BF16, TM_DTYPE_F32, call, ptr
+from treemoe_spec_amd._capi import TM_DTYPE_BF16, TM_DTYPE_F32, call, check, ptr
 from treemoe_spec_amd.kv_cache import device_tables_of, scratch_pages_of
+
+# The per-step greedy path calls the C ABI through the CPython binding when it
+# is built (one Python-to-C transition per entry point instead of ctypes'
+# per-argument conversions); the ctypes binding serves every other call.
+try:
+    from treemoe_spec_amd import _tmfast as _fast
+except ImportError:  # not built: the ctypes binding is used
+    _fast = None
 
 
 @dataclass
@@ -55,15 +65,54 @@ def argmax_workspace(n: int, device) -> torch.Tensor:
 
 
 class _Scratch:
-    """Per (N, device) internal buffers of the greedy path, reused by every
-    call on that device (stream-ordered, like the reference's workspaces):
-    the argmax row partials and the int32 argmax vector."""
+    """Per (N, device) internal buffers, reused by every call on that device
+    (stream-ordered, like the reference's workspaces): the argmax row
+    partials, the int32 argmax vector, and the pinned host word the KV commit
+    writes num_accepted into (created on first use)."""
 
-    __slots__ = ("partials", "argmax")
+    __slots__ = ("partials", "argmax", "note", "note_np", "note_dev")
 
     def __init__(self, n: int, device):
         self.partials = argmax_workspace(n, device)
         self.argmax = torch.empty(n, dtype=torch.int32, device=device)
+        self.note = None
+
+    def host_count(self) -> int:
+        """Device address of the pinned count word (0 if unavailable)."""
+        if self.note is None:
+            self.note = torch.full((1,), -1, dtype=torch.int64, pin_memory=True)
+            self.note_np = self.note.numpy()
+            addr = ctypes.c_void_p()
+            rc = _capi.lib().tm_host_device_pointer(ctypes.c_void_p(self.note.data_ptr()),
+                                                    ctypes.byref(addr))
+            self.note_dev = addr.value if rc == 0 and addr.value else 0
+        return self.note_dev
+
+
+# How long the host spins on the pinned count word before it falls back to a
+# stream synchronisation (queued work ahead of op4 can delay the word).
+_NOTE_SPIN_S = 2e-3
+
+
+def _read_count(ws: _Scratch, result: torch.Tensor) -> int:
+    """num_accepted as written by the KV commit into the pinned word; after
+    _NOTE_SPIN_S, or when no word was passed, a synchronising read of
+    result[1] (what the reference does, op4_commit.py:267)."""
+    if ws.note_dev:
+        note = ws.note_np
+        deadline = time.perf_counter() + _NOTE_SPIN_S
+        while True:
+            for _ in range(256):
+                v = int(note[0])
+                if v >= 0:
+                    return v
+            if time.perf_counter() > deadline:
+                break
+        torch.cuda.current_stream(result.device).synchronize()
+        v = int(note[0])
+        if v >= 0:
+            return v
+    return int(result[1])
 
 
 _scratch_cache: dict[tuple, _Scratch] = {}
@@ -147,7 +196,7 @@ def _cached_csr(children: list[list[int]], n: int, device) -> tuple[torch.Tensor
 
 
 def _commit(kv, res_slots: torch.Tensor, result: torch.Tensor, n: int, commit_depth: int,
-            dev, stream: int) -> None:
+            dev, stream: int, host_count: int = 0) -> None:
     """Copy the KV rows of [root] + accepted path from the tree scratch to
     positions seq_len, seq_len + 1, ... on the device; advance seq_len."""
     tree_pages = scratch_pages_of(kv)
@@ -158,10 +207,14 @@ def _commit(kv, res_slots: torch.Tensor, result: torch.Tensor, n: int, commit_de
         raise ValueError("tree larger than the KV scratch pages")
     kv._ensure_capacity(kv.seq_len + commit_depth + 1)   # reference :251
     table, scratch = device_tables_of(kv, dev)
-    call("tm_op4_kv_commit", ptr(k), ptr(v), k.element_size(), k.shape[0],
-         k.shape[3] * k.shape[4], k.stride(0), k.stride(1), k.stride(2), kv.block_size,
-         ptr(res_slots), ptr(result), ptr(scratch), len(tree_pages), ptr(table),
-         len(kv.block_table), kv.seq_len, commit_depth, stream)
+    args = (ptr(k), ptr(v), k.element_size(), k.shape[0], k.shape[3] * k.shape[4], k.stride(0),
+            k.stride(1), k.stride(2), kv.block_size, ptr(res_slots), ptr(result), ptr(scratch),
+            len(tree_pages), ptr(table), len(kv.block_table), kv.seq_len, commit_depth,
+            host_count, stream)
+    if _fast is not None:
+        check(_fast.kv_commit(*args), "tm_op4_kv_commit")
+    else:
+        call("tm_op4_kv_commit", *args)
 
 
 def _tree_depth(children: list[list[int]]) -> int:
@@ -218,7 +271,7 @@ def fused_verify_commit(
     # allocation holding accepted_slots [N], accepted_tokens [N] and
     # (bonus, num_accepted, next_root)
     out = torch.empty(2 * n + 3, dtype=torch.int64, device=dev)
-    slots, toks, result = out[:n], out[n:2 * n], out[2 * n:]
+    slots, toks, result = out.split((n, n, 3))
     stream = _capi.stream_of(dev)
     c_start, c_count, c_list = ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n
     if temperature != 0.0:
@@ -239,16 +292,26 @@ def fused_verify_commit(
         if rep_penalty != 1.0:
             _apply_rep_penalty(target_logits, dtype, prev_tokens, rep_penalty, stream)
         ws = _scratch(n, dev)
-        call("tm_op4_argmax_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
-             ptr(tokens), c_start, c_count, c_list, num_edges, max_depth,
-             1 if rep_penalty != 1.0 else 0, ptr(ws.argmax),
-             ptr(slots), ptr(toks), ptr(result), ptr(ws.partials), stream)
+        args = (ptr(target_logits), dtype, n, v, target_logits.stride(0), ptr(tokens), c_start,
+                c_count, c_list, num_edges, max_depth, 1 if rep_penalty != 1.0 else 0,
+                ptr(ws.argmax), ptr(slots), ptr(toks), ptr(result), ptr(ws.partials), stream)
+        if _fast is not None:
+            check(_fast.argmax_walk(*args), "tm_op4_argmax_walk")
+        else:
+            call("tm_op4_argmax_walk", *args)
         commit_depth = max_depth
-    res = VerifyResult(accepted_slots=slots, accepted_tokens=toks,
-                       bonus_token=result[0], num_accepted=result[1])
+    bonus, num, _ = result.unbind()
+    res = VerifyResult(accepted_slots=slots, accepted_tokens=toks, bonus_token=bonus,
+                       num_accepted=num)
     if kv is not None:
         # commit [root] + accepted path: the root token's KV (tree slot 0) is
-        # part of the committed sequence too (reference :242-247).
-        _commit(kv, slots, result, n, commit_depth, dev, stream)
-        kv.seq_len += int(res.num_accepted) + 1   # the one D2H, reference :267
+        # part of the committed sequence too (reference :242-247).  The count
+        # comes back through the pinned word the commit writes (reference
+        # :267 reads it with a device-to-host copy).
+        ws = _scratch(n, dev)
+        note = ws.host_count()
+        if note:
+            ws.note_np[0] = -1
+        _commit(kv, slots, result, n, commit_depth, dev, stream, note)
+        kv.seq_len += _read_count(ws, result) + 1
     return res
