@@ -42,7 +42,8 @@ extern "C" {
 
 /* Limits checked by the entry points. */
 #define TM_MAX_EXPERTS 64
-#define TM_MAX_TOKENS 4096
+#define TM_MAX_TOKENS 65536     /* tokens per op1 layer (routing); the GEMMs also need their
+                                    byte offsets below 2^31 */
 #define TM_GEMM_TILE_M 64      /* rows of one expert processed per GEMM tile */
 #define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
 #define TM_OP4_NOALLOC_MAX_NODES 2048  /* N limit of tm_op4_argmax_walk_noalloc */

@@ -94,6 +94,62 @@ def test_route_bucket_bit_exact(seed, t, budget, objective, accept_kind):
         assert np.array_equal(demand.cpu().numpy().view(np.uint32), ref.demand.view(np.uint32))
 
 
+@pytest.mark.parametrize("t,e,budget,objective,block_m", [
+    (4097, 8, 4, "mass", 16), (8192, 8, 2, "critical_path", 32), (8192, 8, 8, "mass", 16),
+    (20000, 8, 4, "critical_path", 16), (5000, 64, 32, "mass", 32),
+    (9001, 64, 5, "critical_path", 16)])
+def test_route_many_tokens_bit_exact(t, e, budget, objective, block_m):
+    """More tokens than the LDS-resident bucketing holds (4096) go through the
+    many-token kernel: every routing output bit-exact against the oracle."""
+    _say(f"route many tokens t={t} E={e} B={budget} {objective} BM={block_m}")
+    m = _op1()
+    g = torch.Generator().manual_seed(t + e)
+    gates = torch.softmax(torch.randn(t, e, generator=g) * 2, -1)
+    accept = torch.rand(t, generator=g)
+    accept[::7] = 0.01  # some tokens below tau
+    x = torch.zeros(t, 256, dtype=torch.bfloat16)
+    router = torch.zeros(e, 256, dtype=torch.bfloat16)
+    ids, w, padded, blk, s2r, max_blocks, demand = m.route_and_bucket(
+        x.cuda(), router.cuda(), accept.cuda(), budget, block_m=block_m, return_demand=True,
+        router_gates=gates.cuda(), routing_objective=objective)
+    ref = oracle_c.route_bucket(gates.numpy(), accept.numpy(), budget, objective=objective,
+                                block_m=block_m)
+    assert max_blocks == ref.max_blocks
+    assert np.array_equal(ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+    assert np.array_equal(w.reshape(-1).cpu().numpy().view(np.uint32),
+                          ref.gates_flat.view(np.uint32))
+    assert np.array_equal(padded.cpu().numpy(), ref.padded_slots)
+    assert np.array_equal(blk.cpu().numpy(), ref.block_expert_ids)
+    assert np.array_equal(s2r.cpu().numpy(), ref.slot_to_row)
+    assert np.array_equal(demand.cpu().numpy().view(np.uint32), ref.demand.view(np.uint32))
+
+
+def test_route_experts_many_tokens_layout():
+    """route_experts at T = 8192 (router + many-token bucketing): the compact
+    layout the GEMMs consume equals the oracle's."""
+    _say("route_experts t=8192")
+    m = _op1()
+    t, e, h = 8192, 8, 512
+    x, router, accept = _route_case(11, t, e, h, 4, "mass", "uniform")
+    r = m.route_experts(x.cuda(), router.cuda(), accept.cuda(), 4, inter=512)
+    gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(router))
+    ref = oracle_c.route_bucket(gates, accept.numpy(), 4)
+    assert np.array_equal(r.topk_ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+    assert np.array_equal(r.sorted_slots.cpu().numpy(), ref.sorted_slots)
+    assert np.array_equal(r.slot_pos.cpu().numpy(), ref.slot_pos)
+    assert np.array_equal(r.expert_offsets.cpu().numpy(), ref.expert_offsets)
+    assert np.array_equal(r.tiles.cpu().numpy(), ref.tiles)
+
+
+def test_forward_many_tokens_matches_golden():
+    """A layer of 6000 tokens (more than the LDS-resident bucketing holds)
+    end to end against the FP64 golden."""
+    _say("forward t=6000")
+    out, golden, _, _ = _forward_and_golden(6000, 8, 256, 512, 4, 31)
+    err = op1_ref.rel_l2(out.cpu().float(), golden)
+    assert err <= REL_L2_TOL, err
+
+
 @pytest.mark.parametrize("t", [7, 64, 2048])
 @pytest.mark.parametrize("budget", [2, 4, 8])
 def test_bucket_from_given_gates_bit_exact(t, budget):

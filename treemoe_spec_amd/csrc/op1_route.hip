@@ -19,7 +19,10 @@ namespace {
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxSlots = 2 * TM_MAX_TOKENS;
+// The bucketing kernel keeps every per-slot intermediate in LDS up to this
+// many tokens; larger layers use tm_bucket_large_kernel.
+constexpr int kLdsMaxTokens = 4096;
+constexpr int kMaxSlots = 2 * kLdsMaxTokens;
 constexpr int kMaxChunks = kMaxSlots / 64;
 constexpr int kMaxPaddedRows = 16384;
 // Tokens from which the row router runs: its per-workgroup W_g copy costs
@@ -116,7 +119,7 @@ constexpr int kMaxBlocks = kMaxPaddedRows / 16;
 
 struct BucketShared {
   float gates[kStageFloats];
-  float accept[TM_MAX_TOKENS];
+  float accept[kLdsMaxTokens];
   float demand[TM_MAX_EXPERTS];
   float crit[TM_MAX_EXPERTS];
   int count[TM_MAX_EXPERTS];
@@ -467,14 +470,231 @@ __global__ void __launch_bounds__(kThreads) tm_bucket_kernel(BucketArgs args) {
   bucket_all(args, sh);
 }
 
+// ------------------------------------------------------ many tokens --
+// The same budget routing and bucketing for T > kLdsMaxTokens, whose per-slot
+// intermediates do not fit LDS.  One workgroup of 1024 threads, the phases and
+// every floating-point operation in the order of bucket_all (so the outputs
+// equal what bucket_all would compute); the intermediates live in the output
+// buffers, each overwritten by its final value after its last use:
+//   expert of slot s           topk_ids[s]                  (final in phase 3)
+//   rank of s in its chunk     slot_pos[s] -> its position  (final in 4d)
+//   per-chunk expert counts    slot_to_row, as int32 words  (final in 4d)
+//   expert of padded block b   block_expert_ids[b]          (final in 4c)
+//   compact order              sorted_slots                 (final in 4d)
+// Phases exchange data through global memory, so they are separated by
+// __syncthreads() (its workgroup-scope release/acquire orders the stores and
+// loads of the workgroup's waves).
+constexpr int kLargeThreads = 1024;
+constexpr int kLargeWaves = kLargeThreads / 64;
+
+__global__ void __launch_bounds__(kLargeThreads) tm_bucket_large_kernel(BucketArgs a) {
+  __shared__ float s_demand[TM_MAX_EXPERTS], s_crit[TM_MAX_EXPERTS];
+  __shared__ int s_count[TM_MAX_EXPERTS], s_block_start[TM_MAX_EXPERTS + 1];
+  __shared__ int s_offset[TM_MAX_EXPERTS + 1], s_tile_start[TM_MAX_EXPERTS + 1];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int T = a.T, E = a.E;
+  const int nslot = 2 * T;
+  const int nchunk = (nslot + 63) >> 6;
+  const int padded_rows = a.max_blocks * a.BM;
+  const bool critical = a.objective == TM_OBJECTIVE_CRITICAL_PATH;
+  const float* G = a.gates;
+  int64_t* fe = a.topk_ids;                                 // expert of slot s
+  int32_t* cnt = reinterpret_cast<int32_t*>(a.slot_to_row); // [nchunk][E], 4T words
+
+  if (critical) {  // unrestricted top-1 / top-2 of every token
+    for (int t = tid; t < T; t += kLargeThreads) {
+      const float* g = G + (size_t)t * E;
+      Top2 r{-1, -1, 0.0f, 0.0f};
+      for (int e = 0; e < E; ++e) r.offer(g[e], e);
+      fe[2 * t] = r.i1;
+      fe[2 * t + 1] = r.i2;
+    }
+    __syncthreads();
+  }
+  // 1. demand (and criticality): lane-strided partials in token order, xor fold
+  for (int e = wave; e < E; e += kLargeWaves) {
+    float acc = 0.0f;
+    float crit = -INFINITY;
+    for (int t = lane; t < T; t += 64) {
+      const float av = a.accept[t];
+      const float p = av * G[(size_t)t * E + e];
+      acc = acc + p;
+      if (critical) {
+        const bool needed = (fe[2 * t] == e) || ((fe[2 * t + 1] == e) && (av >= a.tau));
+        if (needed) crit = fmaxf(crit, av);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      acc = acc + __shfl_xor(acc, off);
+      crit = fmaxf(crit, __shfl_xor(crit, off));
+    }
+    if (lane == 0) {
+      s_demand[e] = acc;
+      s_crit[e] = crit;
+      a.demand_out[e] = acc;
+    }
+  }
+  __syncthreads();
+  // 2. keep set (every wave; as in bucket_all)
+  unsigned long long keep;
+  {
+    const float d = lane < E ? s_demand[lane] : 0.0f;
+    const float c = (critical && lane < E) ? s_crit[lane] : 0.0f;
+    int rank = 0;
+    for (int f = 0; f < E; ++f) {
+      const float df = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d), f));
+      const float cf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), f));
+      bool before;
+      if (critical && cf != c) {
+        before = cf > c;
+      } else if (df != d) {
+        before = df > d;
+      } else {
+        before = f < lane;
+      }
+      rank += before ? 1 : 0;
+    }
+    keep = __ballot(lane < E && rank < a.budget);
+  }
+  // 3. in-budget top-2, renormalisation, degrade
+  for (int t = tid; t < T; t += kLargeThreads) {
+    const float* g = G + (size_t)t * E;
+    Top2 r{-1, -1, 0.0f, 0.0f};
+    for (int e = 0; e < E; ++e) r.offer(((keep >> e) & 1ull) ? g[e] : 0.0f, e);
+    const float s = r.g1 + r.g2;
+    float tg1 = r.g1 / s;
+    float tg2 = r.g2 / s;
+    if (a.accept[t] < a.tau) { tg1 = 1.0f; tg2 = 0.0f; }
+    fe[2 * t] = r.i1;
+    fe[2 * t + 1] = r.i2;
+    a.gates_flat[2 * t] = tg1;
+    a.gates_flat[2 * t + 1] = tg2;
+  }
+  __syncthreads();
+  // 4a. per-chunk expert counts and in-chunk ranks from ballots
+  for (int q = wave; q < nchunk; q += kLargeWaves) {
+    const int sl = q * 64 + lane;
+    const int f = (sl < nslot) ? (int)fe[sl] : -1;
+    int mycnt = 0, inrank = 0;
+    for (int e = 0; e < E; ++e) {
+      const unsigned long long m = __ballot(f == e);
+      if (lane == e) mycnt = __popcll(m);
+      if (f == e) inrank = __popcll(m & ((1ull << lane) - 1ull));
+    }
+    if (lane < E) cnt[(size_t)q * E + lane] = mycnt;
+    if (sl < nslot) a.slot_pos[sl] = inrank;
+  }
+  __syncthreads();
+  // 4b. exclusive scan over chunks (slot order) per expert, 64 chunks per step
+  for (int e = wave; e < E; e += kLargeWaves) {
+    int carry = 0;
+    for (int q0 = 0; q0 < nchunk; q0 += 64) {
+      const int q = q0 + lane;
+      const int v = (q < nchunk) ? cnt[(size_t)q * E + e] : 0;
+      int tot;
+      const int x = wave_exclusive_scan(v, lane, &tot);
+      if (q < nchunk) cnt[(size_t)q * E + e] = carry + x;
+      carry += tot;
+    }
+    if (lane == 0) s_count[e] = carry;
+  }
+  __syncthreads();
+  // 4c. offsets, block starts and tile starts (wave 0, lane = expert)
+  if (wave == 0) {
+    const int c = (lane < E) ? s_count[lane] : 0;
+    int tot_off, tot_blk, tot_tiles;
+    const int off = wave_exclusive_scan(c, lane, &tot_off);
+    const int bs = wave_exclusive_scan((c + a.BM - 1) / a.BM, lane, &tot_blk);
+    const int ts = wave_exclusive_scan((c + TM_GEMM_TILE_M - 1) / TM_GEMM_TILE_M, lane, &tot_tiles);
+    if (lane < E) {
+      s_offset[lane] = off;
+      s_block_start[lane] = bs;
+      s_tile_start[lane] = ts;
+      a.expert_offsets[lane] = off;
+    }
+    if (lane == 0) {
+      s_offset[E] = tot_off;
+      s_block_start[E] = tot_blk;
+      s_tile_start[E] = tot_tiles;
+      a.expert_offsets[E] = tot_off;
+    }
+  }
+  __syncthreads();
+  // owners of the padded blocks and the GEMM tiles, one thread per entry
+  for (int b = tid; b < a.max_blocks; b += kLargeThreads) {
+    int owner = -1;
+    for (int e = 0; e < E; ++e)
+      if (b >= s_block_start[e] && b < s_block_start[e + 1]) owner = e;
+    a.block_expert_ids[b] = owner;
+  }
+  for (int j = tid; j < a.max_tiles; j += kLargeThreads) {
+    int e = -1;
+    for (int k = 0; k < E; ++k)
+      if (j >= s_tile_start[k] && j < s_tile_start[k + 1]) e = k;
+    int32_t* tl = a.tiles + 4 * j;
+    if (e >= 0) {
+      const int k = j - s_tile_start[e];
+      tl[0] = e;
+      tl[1] = s_offset[e] + k * TM_GEMM_TILE_M;
+      tl[2] = min(TM_GEMM_TILE_M, s_count[e] - k * TM_GEMM_TILE_M);
+    } else {
+      tl[0] = -1;
+      tl[1] = 0;
+      tl[2] = 0;
+    }
+    tl[3] = 0;
+  }
+  // 4d. positions (slot_pos holds the in-chunk rank until its own thread
+  //     replaces it), then the compact order and the padded rows of the slots
+  for (int sl = tid; sl < nslot; sl += kLargeThreads) {
+    const int f = (int)fe[sl];
+    const int rank = cnt[(size_t)(sl >> 6) * E + f] + a.slot_pos[sl];
+    a.slot_pos[sl] = s_offset[f] + rank;
+  }
+  __syncthreads();
+  for (int sl = tid; sl < nslot; sl += kLargeThreads) {
+    const int f = (int)fe[sl];
+    const int pos = a.slot_pos[sl];
+    a.slot_to_row[sl] = (int64_t)s_block_start[f] * a.BM + (pos - s_offset[f]);
+    a.sorted_slots[pos] = sl;
+  }
+  __syncthreads();
+  // 4e. padded rows
+  for (int i = tid; i < padded_rows; i += kLargeThreads) {
+    const int e = (int)a.block_expert_ids[i / a.BM];
+    int64_t slot = -1;
+    if (e >= 0) {
+      const int rank = i - s_block_start[e] * a.BM;
+      if (rank < s_count[e]) slot = a.sorted_slots[s_offset[e] + rank];
+    }
+    a.padded_slots[i] = slot;
+  }
+}
+
 int check_bucket_args(int64_t T, int64_t E, int64_t budget, int objective, int64_t block_m,
                       int64_t max_blocks, int64_t max_tiles) {
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS) return TM_ERR_SHAPE;
   if (budget < 2 || budget > E) return TM_ERR_ARG;
   if (objective != TM_OBJECTIVE_MASS && objective != TM_OBJECTIVE_CRITICAL_PATH) return TM_ERR_ARG;
   if (block_m != 16 && block_m != 32) return TM_ERR_ARG;
-  if (max_blocks < 1 || max_blocks * block_m > kMaxPaddedRows || max_tiles < 1) return TM_ERR_SHAPE;
+  if (max_blocks < 1 || max_tiles < 1) return TM_ERR_SHAPE;
+  if (T <= kLdsMaxTokens ? max_blocks * block_m > kMaxPaddedRows
+                         : max_blocks * block_m > (int64_t)1 << 30)
+    return TM_ERR_SHAPE;
   return TM_OK;
+}
+
+// The bucketing launch for T tokens: LDS-resident up to kLdsMaxTokens (and
+// kMaxPaddedRows padded rows), else the many-token kernel.
+void launch_bucket(const BucketArgs& a, hipStream_t stream) {
+  if (a.T <= kLdsMaxTokens && a.max_blocks * a.BM <= kMaxPaddedRows) {
+    hipLaunchKernelGGL(tm_bucket_kernel, dim3(1), dim3(kThreads), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL(tm_bucket_large_kernel, dim3(1), dim3(kLargeThreads), 0, stream, a);
+  }
 }
 
 BucketArgs make_args(const float* gates, const float* accept, int64_t T, int64_t E,
@@ -534,7 +754,7 @@ extern "C" int tm_op1_route_bucket(const float* gates, const float* accept, int6
                                  max_tiles, topk_ids, gates_flat, padded_slots,
                                  block_expert_ids, slot_to_row, demand, expert_offsets,
                                  sorted_slots, slot_pos, tiles);
-  hipLaunchKernelGGL(tm_bucket_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, a);
+  launch_bucket(a, (hipStream_t)stream);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
@@ -558,7 +778,7 @@ extern "C" int tm_op1_route(const void* x, const void* wg, const float* accept, 
   launch_router((const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E,
                 (hipStream_t)stream);
   TM_HIP_CHECK_LAUNCH();
-  hipLaunchKernelGGL(tm_bucket_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, a);
+  launch_bucket(a, (hipStream_t)stream);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
