@@ -106,15 +106,15 @@ def kernel_breakdown(m, inp, reps: int) -> dict:
         ev[r][1].record()
         _capi.call("tm_op1_gemm1", x.data_ptr(), w1.data_ptr(), w3.data_ptr(), ws.h.data_ptr(),
                    routing.sorted_slots.data_ptr(), routing.tiles.data_ptr(),
-                   routing.max_tiles, n, hidden, inter, e, stream)
+                   routing.max_tiles, n, hidden, inter, e, _capi.TM_DTYPE_BF16, stream)
         ev[r][2].record()
         _capi.call("tm_op1_gemm2", ws.h.data_ptr(), w2.data_ptr(), ws.partial.data_ptr(),
                    routing.gates_flat.data_ptr(), routing.sorted_slots.data_ptr(),
                    routing.tiles.data_ptr(), routing.max_tiles, ws.split, n, hidden, inter, e,
-                   stream)
+                   _capi.TM_DTYPE_BF16, stream)
         ev[r][3].record()
         _capi.call("tm_op1_combine", ws.partial.data_ptr(), routing.slot_pos.data_ptr(),
-                   out.data_ptr(), n, hidden, ws.split, stream)
+                   out.data_ptr(), n, hidden, ws.split, _capi.TM_DTYPE_BF16, stream)
         ev[r][4].record()
     torch.cuda.synchronize()
     res = {}

@@ -39,6 +39,7 @@ extern "C" {
 
 #define TM_DTYPE_F32 0
 #define TM_DTYPE_BF16 1
+#define TM_DTYPE_F16 2
 
 /* Limits checked by the entry points. */
 #define TM_MAX_EXPERTS 64
@@ -48,9 +49,11 @@ extern "C" {
 #define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
 #define TM_OP4_NOALLOC_MAX_NODES 2048  /* N limit of tm_op4_argmax_walk_noalloc */
 
-/* ABI version (major*10000 + minor*100 + patch): 3.0.0.  Version 2 added
+/* ABI version (major*10000 + minor*100 + patch): 4.0.0.  Version 2 added
  * num_edges to tm_op4_argmax_walk / tm_op4_sample_walk and softmax_argmax to
- * tm_op4_argmax_walk; version 3 added host_count to tm_op4_kv_commit. */
+ * tm_op4_argmax_walk; version 3 added host_count to tm_op4_kv_commit;
+ * version 4 added `dtype` (TM_DTYPE_BF16 or TM_DTYPE_F16) to the op1 entry
+ * points that read or write 16-bit activations or weights. */
 int tm_version(void);
 
 /* Human-readable text for a return code of any entry point. */
@@ -63,6 +66,12 @@ int tm_host_device_pointer(void* host, void** device);
 
 /* ---------------------------------------------------------------- op1 -- */
 
+/* `dtype` of the op1 entry points is the type of x, the weights, h and the
+ * output: TM_DTYPE_BF16 or TM_DTYPE_F16 (the reference kernels take either,
+ * treemoe/kernels/op1_tree_moe.py:762-766); "bf16" below stands for it.
+ * Arithmetic is fp32 in both cases; rounding to the type is
+ * round-to-nearest-even. */
+
 /*
  * Router: gates[t, e] = softmax_e( bf16( x[t, :] . wg[e, :] ) ), fp32.
  * Replaces `F.linear(x, W_g)` + `torch.softmax(logits.float(), -1)` at
@@ -72,7 +81,7 @@ int tm_host_device_pointer(void* host, void** device);
  * 2 <= E <= TM_MAX_EXPERTS.
  */
 int tm_op1_router_gates(const void* x, const void* wg, int64_t T, int64_t H,
-                        int64_t E, float* gates, void* stream);
+                        int64_t E, float* gates, int dtype, void* stream);
 
 /*
  * Budget routing + stable (expert, DFS) bucketing in one workgroup.
@@ -120,7 +129,7 @@ int tm_op1_route(const void* x, const void* wg, const float* accept, int64_t T,
                  int64_t* padded_slots, int64_t* block_expert_ids,
                  int64_t* slot_to_row, float* demand, int32_t* expert_offsets,
                  int32_t* sorted_slots, int32_t* slot_pos, int32_t* tiles,
-                 void* stream);
+                 int dtype, void* stream);
 
 /*
  * Gate/up projection + SwiGLU for every routed slot.
@@ -136,7 +145,7 @@ int tm_op1_route(const void* x, const void* wg, const float* accept, int64_t T,
 int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void* h,
                  const int32_t* sorted_slots, const int32_t* tiles,
                  int64_t max_tiles, int64_t T, int64_t H, int64_t I, int64_t E,
-                 void* stream);
+                 int dtype, void* stream);
 
 /*
  * Down projection, split over K = I into `split` deterministic segments.
@@ -149,7 +158,7 @@ int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void* h,
 int tm_op1_gemm2(const void* h, const void* w2, float* y,
                  const float* gates_flat, const int32_t* sorted_slots,
                  const int32_t* tiles, int64_t max_tiles, int64_t split,
-                 int64_t T, int64_t H, int64_t I, int64_t E, void* stream);
+                 int64_t T, int64_t H, int64_t I, int64_t E, int dtype, void* stream);
 
 /*
  * Fixed-order combine.  Replaces `_combine_kernel`
@@ -158,7 +167,7 @@ int tm_op1_gemm2(const void* h, const void* w2, float* y,
  * with p_k = slot_pos[2t + k].  out: [T, H] bf16.  Requires H % 4 == 0.
  */
 int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
-                   int64_t T, int64_t H, int64_t split, void* stream);
+                   int64_t T, int64_t H, int64_t split, int dtype, void* stream);
 
 /*
  * Gate/up projection + SwiGLU for many rows per expert (prefill / batched
@@ -176,7 +185,7 @@ int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
 int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w3, void* h,
                          const int32_t* sorted_slots, const int32_t* expert_offsets,
                          const int32_t* tiles, int64_t max_tiles, int64_t T, int64_t H,
-                         int64_t I, int64_t E, void* stream);
+                         int64_t I, int64_t E, int dtype, void* stream);
 
 /*
  * Down projection for many rows per expert, MFMA-tiled over 128 rows x 256
@@ -191,7 +200,7 @@ int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w3, void* h,
 int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y, const float* gates_flat,
                          const int32_t* sorted_slots, const int32_t* expert_offsets,
                          const int32_t* tiles, int64_t max_tiles, int64_t split, int64_t T,
-                         int64_t H, int64_t I, int64_t E, void* stream);
+                         int64_t H, int64_t I, int64_t E, int dtype, void* stream);
 
 /* ---------------------------------------------------------------- op4 -- */
 

@@ -41,6 +41,53 @@ static uint16_t f32_to_bf16_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
+static float f16_bits_to_f32(uint16_t b) {
+  const uint32_t sign = ((uint32_t)b & 0x8000u) << 16;
+  const uint32_t ex = ((uint32_t)b >> 10) & 0x1fu;
+  const uint32_t man = (uint32_t)b & 0x3ffu;
+  uint32_t u;
+  if (ex == 0x1fu) {
+    u = sign | 0x7f800000u | (man << 13);            /* inf / NaN */
+  } else if (ex != 0) {
+    u = sign | ((ex + 112u) << 23) | (man << 13);    /* normal: rebias 15 -> 127 */
+  } else {                                           /* zero / subnormal: man * 2^-24 */
+    float f = (float)man * 5.9604644775390625e-08f;  /* exact: man < 2^10 */
+    memcpy(&u, &f, 4);
+    u |= sign;
+  }
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+/* round-to-nearest-even float -> IEEE half bits: overflow (|f| >= 65520) to
+ * infinity, subnormal results kept, NaN quiet */
+static uint16_t f32_to_f16_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  const uint32_t sign = (u >> 16) & 0x8000u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((a >> 13) & 0x3ffu));
+  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);
+  if (a >= 0x38800000u) {            /* normal half: |f| >= 2^-14 */
+    uint32_t m = a - 0x38000000u;    /* exponent rebias 127 -> 15 */
+    m += 0xfffu + ((m >> 13) & 1u);  /* round the 13 dropped bits to nearest even */
+    return (uint16_t)(sign | (m >> 13));
+  }
+  float af;                          /* subnormal half: round |f| / 2^-24 to an integer */
+  memcpy(&af, &a, 4);
+  return (uint16_t)(sign | (uint32_t)rintf(af * 16777216.0f));
+}
+
+/* fp32 -> fp16 bits for n values (the rounding the fp16 router and GEMM
+ * epilogues apply) */
+void orc_f32_to_f16(const float* in, int64_t n, uint16_t* out) {
+  for (int64_t i = 0; i < n; ++i) out[i] = f32_to_f16_bits(in[i]);
+}
+
+static float half_to_f32(uint16_t b, int f16) { return f16 ? f16_bits_to_f32(b) : bf16_bits_to_f32(b); }
+static uint16_t f32_to_half(float f, int f16) { return f16 ? f32_to_f16_bits(f) : f32_to_bf16_bits(f); }
+
 static float scale_pow2(float p, int k) {
   uint32_t bits = (uint32_t)(k + 127) << 23;
   float s;
@@ -74,38 +121,45 @@ static float fold64(float* s) {
   return s[0];
 }
 
-/* bf16 bits of the router logit x[t] . wg[e]: 64 lane partials over 8-element
- * chunks (chunk c to lane c % 64, fused multiply-adds in chunk order), the
- * pairwise fold, then round to bf16. */
+/* bits of the router logit x[t] . wg[e] in the inputs' 16-bit type (bf16, or
+ * fp16 when f16): 64 lane partials over 8-element chunks (chunk c to lane
+ * c % 64, fused multiply-adds in chunk order), the pairwise fold, then round
+ * to the type. */
 static uint16_t router_logit_bits(const uint16_t* x, const uint16_t* wg, int64_t t, int64_t e,
-                                  int64_t H) {
+                                  int64_t H, int f16) {
   float part[ORC_LANES];
   for (int l = 0; l < ORC_LANES; ++l) part[l] = 0.0f;
   for (int64_t c = 0; c < H / 8; ++c) {
     const int l = (int)(c % ORC_LANES);
     for (int j = 0; j < 8; ++j) {
-      const float a = bf16_bits_to_f32(x[t * H + 8 * c + j]);
-      const float b = bf16_bits_to_f32(wg[e * H + 8 * c + j]);
+      const float a = half_to_f32(x[t * H + 8 * c + j], f16);
+      const float b = half_to_f32(wg[e * H + 8 * c + j], f16);
       part[l] = fmaf(a, b, part[l]);
     }
   }
-  return f32_to_bf16_bits(fold64(part));
+  return f32_to_half(fold64(part), f16);
 }
 
-/* logits[t, e] (bf16 bits) as the router computes them before the softmax */
+/* logits[t, e] (bits of the 16-bit type) as the router computes them before
+ * the softmax */
+void orc_router_logits_dt(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t H,
+                          int64_t E, int f16, uint16_t* logits) {
+  for (int64_t t = 0; t < T; ++t)
+    for (int64_t e = 0; e < E; ++e) logits[t * E + e] = router_logit_bits(x, wg, t, e, H, f16);
+}
+
 void orc_router_logits(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t H, int64_t E,
                        uint16_t* logits) {
-  for (int64_t t = 0; t < T; ++t)
-    for (int64_t e = 0; e < E; ++e) logits[t * E + e] = router_logit_bits(x, wg, t, e, H);
+  orc_router_logits_dt(x, wg, T, H, E, 0, logits);
 }
 
-/* gates[t, e] = softmax(bf16(x[t] . wg[e])) */
-void orc_router_gates(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t H, int64_t E,
-                      float* gates) {
+/* gates[t, e] = softmax(round16(x[t] . wg[e])), round16 to bf16 or fp16 */
+void orc_router_gates_dt(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t H,
+                         int64_t E, int f16, float* gates) {
   float logits[64];
   for (int64_t t = 0; t < T; ++t) {
     for (int64_t e = 0; e < E; ++e)
-      logits[e] = bf16_bits_to_f32(router_logit_bits(x, wg, t, e, H));
+      logits[e] = half_to_f32(router_logit_bits(x, wg, t, e, H, f16), f16);
     float m = -INFINITY;
     for (int64_t e = 0; e < E; ++e) m = fmaxf(m, logits[e]);
     float ex[64];
@@ -116,6 +170,11 @@ void orc_router_gates(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t 
     for (int64_t e = 0; e < E; ++e) sum = sum + ex[e];
     for (int64_t e = 0; e < E; ++e) gates[t * E + e] = ex[e] / sum;
   }
+}
+
+void orc_router_gates(const uint16_t* x, const uint16_t* wg, int64_t T, int64_t H, int64_t E,
+                      float* gates) {
+  orc_router_gates_dt(x, wg, T, H, E, 0, gates);
 }
 
 /*

@@ -33,6 +33,12 @@ def _load():
         lib.orc_router_gates.argtypes = [P, P, I64, I64, I64, P]
         lib.orc_router_logits.restype = None
         lib.orc_router_logits.argtypes = [P, P, I64, I64, I64, P]
+        lib.orc_router_gates_dt.restype = None
+        lib.orc_router_gates_dt.argtypes = [P, P, I64, I64, I64, ctypes.c_int, P]
+        lib.orc_router_logits_dt.restype = None
+        lib.orc_router_logits_dt.argtypes = [P, P, I64, I64, I64, ctypes.c_int, P]
+        lib.orc_f32_to_f16.restype = None
+        lib.orc_f32_to_f16.argtypes = [P, I64, P]
         lib.orc_route_bucket.restype = ctypes.c_int
         lib.orc_route_bucket.argtypes = [P, P, I64, I64, I64, ctypes.c_float, ctypes.c_int,
                                          I64, I64, I64] + [P] * 10
@@ -63,28 +69,38 @@ def expf_array(x: np.ndarray) -> np.ndarray:
                     dtype=np.float32).reshape(x.shape)
 
 
-def router_gates(x_bf16_bits: np.ndarray, wg_bf16_bits: np.ndarray) -> np.ndarray:
-    """gates [T, E] fp32 from bf16 bit patterns (uint16) of x [T, H] and W_g [E, H]."""
-    x = np.ascontiguousarray(x_bf16_bits, dtype=np.uint16)
-    w = np.ascontiguousarray(wg_bf16_bits, dtype=np.uint16)
+def router_gates(x_bits: np.ndarray, wg_bits: np.ndarray, f16: bool = False) -> np.ndarray:
+    """gates [T, E] fp32 from the 16-bit bit patterns (uint16) of x [T, H] and
+    W_g [E, H]: bf16, or fp16 when ``f16``."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(wg_bits, dtype=np.uint16)
     t, h = x.shape
     e = w.shape[0]
     assert w.shape[1] == h and h % 8 == 0 and e <= 64
     out = np.empty((t, e), dtype=np.float32)
-    _load().orc_router_gates(_ptr(x), _ptr(w), t, h, e, _ptr(out))
+    _load().orc_router_gates_dt(_ptr(x), _ptr(w), t, h, e, 1 if f16 else 0, _ptr(out))
     return out
 
 
-def router_logits(x_bf16_bits: np.ndarray, wg_bf16_bits: np.ndarray) -> np.ndarray:
-    """bf16 bits (uint16) of the router logits [T, E] behind router_gates."""
-    x = np.ascontiguousarray(x_bf16_bits, dtype=np.uint16)
-    w = np.ascontiguousarray(wg_bf16_bits, dtype=np.uint16)
+def router_logits(x_bits: np.ndarray, wg_bits: np.ndarray, f16: bool = False) -> np.ndarray:
+    """Bits (uint16, bf16 or fp16) of the router logits [T, E] behind router_gates."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    w = np.ascontiguousarray(wg_bits, dtype=np.uint16)
     t, h = x.shape
     e = w.shape[0]
     assert w.shape[1] == h and h % 8 == 0
     out = np.empty((t, e), dtype=np.uint16)
-    _load().orc_router_logits(_ptr(x), _ptr(w), t, h, e, _ptr(out))
+    _load().orc_router_logits_dt(_ptr(x), _ptr(w), t, h, e, 1 if f16 else 0, _ptr(out))
     return out
+
+
+def f32_to_f16_bits(values: np.ndarray) -> np.ndarray:
+    """IEEE half bits of fp32 values, round to nearest even (the oracle's
+    rounding for fp16 logits and outputs)."""
+    v = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    out = np.empty(v.size, dtype=np.uint16)
+    _load().orc_f32_to_f16(_ptr(v), v.size, _ptr(out))
+    return out.reshape(np.shape(values))
 
 
 def compact_block_limit(num_slots: int, budget: int, block_m: int) -> int:

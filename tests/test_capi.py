@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
     assert set(_capi.SIGNATURES) <= set(declared_functions())
-    assert lib.tm_version() == 30000
+    assert lib.tm_version() == 40000
 
 
 def test_status_strings():
@@ -101,19 +101,21 @@ def test_tree_attention_plan():
 
 
 @pytest.mark.parametrize("call,expect", [
-    (("tm_op1_router_gates", 0, 0, 0, 4096, 8, 0, 0), 1001),          # T = 0
-    (("tm_op1_router_gates", 0, 0, 4, 4095, 8, 0, 0), 1001),          # H % 8
-    (("tm_op1_router_gates", 0, 0, 4, 4096, 65, 0, 0), 1001),         # E > 64
-    (("tm_op1_router_gates", 8, 0, 4, 4096, 8, 0, 0), 1002),          # unaligned x
-    (("tm_op1_gemm1", 0, 0, 0, 0, 0, 0, 1, 64, 4000, 14336, 8, 0), 1001),  # H % 256
-    (("tm_op1_gemm2", 0, 0, 0, 0, 0, 0, 1, 3, 64, 4096, 14336, 8, 0), 1001),  # split
-    (("tm_op1_combine", 0, 0, 0, 64, 4094, 2, 0), 1001),
-    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4000, 14336, 8, 0), 1001),  # H % 64
-    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 0, 2048, 4096, 14336, 8, 0), 1001),  # tiles
-    (("tm_op1_prefill_gemm1", 8, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14336, 8, 0), 1002),  # align
-    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 2, 2048, 4032, 14336, 8, 0), 1001),  # H % 256
-    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14272, 8, 0), 1001),  # I % 128
-    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 3, 2048, 4096, 14336, 8, 0), 1001),  # split
+    (("tm_op1_router_gates", 0, 0, 0, 4096, 8, 0, 1, 0), 1001),          # T = 0
+    (("tm_op1_router_gates", 0, 0, 4, 4095, 8, 0, 1, 0), 1001),          # H % 8
+    (("tm_op1_router_gates", 0, 0, 4, 4096, 65, 0, 1, 0), 1001),         # E > 64
+    (("tm_op1_router_gates", 8, 0, 4, 4096, 8, 0, 1, 0), 1002),          # unaligned x
+    (("tm_op1_router_gates", 0, 0, 4, 4096, 8, 0, 0, 0), 1003),          # fp32 is no op1 dtype
+    (("tm_op1_combine", 0, 0, 0, 64, 4096, 2, 3, 0), 1003),                # unknown dtype
+    (("tm_op1_gemm1", 0, 0, 0, 0, 0, 0, 1, 64, 4000, 14336, 8, 1, 0), 1001),  # H % 256
+    (("tm_op1_gemm2", 0, 0, 0, 0, 0, 0, 1, 3, 64, 4096, 14336, 8, 1, 0), 1001),  # split
+    (("tm_op1_combine", 0, 0, 0, 64, 4094, 2, 1, 0), 1001),
+    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4000, 14336, 8, 1, 0), 1001),  # H % 64
+    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 0, 2048, 4096, 14336, 8, 1, 0), 1001),  # tiles
+    (("tm_op1_prefill_gemm1", 8, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14336, 8, 1, 0), 1002),  # align
+    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 2, 2048, 4032, 14336, 8, 1, 0), 1001),  # H % 256
+    (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14272, 8, 1, 0), 1001),  # I % 128
+    (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 3, 2048, 4096, 14336, 8, 1, 0), 1001),  # split
     (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 3, 1, 0, 0, 0, 0, 0, 0, 0), 1003),
     (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 3, 1, 0, 0, 0, 0, 0, 0, 0), 1001),
     (("tm_op4_argmax_walk", 0, 0, 4, 10, 10, 0, 0, 0, 0, -1, 1, 0, 0, 0, 0, 0, 0, 0), 1001),
@@ -147,8 +149,11 @@ def test_fused_route_argument_errors():
 
     fn = _capi.lib().tm_op1_route
     # x = 8 is misaligned, so every case below fails a check before any launch
-    base = [8, 0, 0, 64, 4096, 8, 4, ctypes.c_float(0.05), 0, 16, 16, 11] + [0] * 12
+    base = [8, 0, 0, 64, 4096, 8, 4, ctypes.c_float(0.05), 0, 16, 16, 11] + [0] * 11 + [1, 0]
     assert fn(*base) == 1002
+    args = list(base)
+    args[-2] = 0
+    assert fn(*args) == 1003                 # fp32 is no op1 dtype
     args = list(base)
     args[4] = 4095
     assert fn(*args) == 1001                 # H % 8

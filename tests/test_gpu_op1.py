@@ -61,6 +61,71 @@ def test_router_gates_bit_exact(t, h, e):
     assert np.array_equal(got.view(np.uint32), expect.view(np.uint32))
 
 
+@pytest.mark.parametrize("t,h,e", [(5, 512, 8), (64, 4096, 8), (2048, 4096, 8),
+                                   (1100, 2048, 16)])
+def test_router_gates_f16_bit_exact(t, h, e):
+    """fp16 operands: logits rounded to fp16 (F.linear on fp16 operands), the
+    softmax in fp32; bit-exact against the oracle on both router kernels."""
+    _say(f"router fp16 t={t} h={h} e={e}")
+    m = _op1()
+    g = torch.Generator().manual_seed(t + h)
+    x = torch.randn(t, h, generator=g).half()
+    router = (torch.randn(e, h, generator=g) * 0.1).half()
+    gates = torch.empty(t, e, dtype=torch.float32, device="cuda")
+    m._launch_router(x.cuda(), router.cuda(), gates)
+    expect = oracle_c.router_gates(bf16_bits(x), bf16_bits(router), f16=True)
+    assert np.array_equal(gates.cpu().numpy().view(np.uint32), expect.view(np.uint32))
+
+
+def _forward_f16(t, e, h, i, budget, seed):
+    m = _op1()
+    g = torch.Generator().manual_seed(seed)
+    x, w1, w2, w3, router, accept = make_moe_inputs(t, e, h, i, g)
+    x, w1, w2, w3, router = (a.half() for a in (x, w1, w2, w3, router))
+    dev = [a.cuda() for a in (x, w1, w2, w3, router, accept)]
+    out = m.tree_moe_forward(*dev, budget)
+    gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(router), f16=True)
+    ref = oracle_c.route_bucket(gates, accept.numpy(), budget)
+    r = m.route_experts(dev[0], dev[4], dev[5], budget, i)
+    assert np.array_equal(r.topk_ids.reshape(-1).cpu().numpy(), ref.topk_ids)
+    golden = op1_ref.expert_ffn_golden(x, w1, w2, w3, torch.from_numpy(ref.topk_ids).view(t, 2),
+                                       torch.from_numpy(ref.gates_flat).view(t, 2))
+    return out, golden
+
+
+@pytest.mark.parametrize("path", ["stream", "tiled"])
+@pytest.mark.parametrize("budget", [4, 8])
+def test_forward_f16_matches_fp64_golden(budget, path, monkeypatch):
+    """fp16 I/O (the reference kernels take fp16 too, op1_tree_moe.py:762-766):
+    fp16 h and output, fp32 accumulation; routing ids equal the oracle's."""
+    _say(f"forward fp16 B={budget} {path}")
+    _force_path(monkeypatch, path)
+    out, golden = _forward_f16(64, 8, 512, 1024, budget, 41 + budget)
+    assert out.dtype == torch.float16
+    err = op1_ref.rel_l2(out.cpu().float(), golden)
+    assert err <= REL_L2_TOL, err
+
+
+@pytest.mark.parametrize("t,h,i", [(64, 4096, 14336), (2048, 512, 1024)])
+def test_forward_f16_large_shapes(t, h, i):
+    """fp16 at the Mixtral layer shape (weight-streaming GEMMs) and at T=2048
+    (the tiled GEMMs with 256-row gate/up tiles)."""
+    _say(f"forward fp16 t={t} h={h} i={i}")
+    out, golden = _forward_f16(t, 8, h, i, 8, 43)
+    err = op1_ref.rel_l2(out.cpu().float(), golden)
+    assert out.dtype == torch.float16 and err <= REL_L2_TOL, err
+
+
+def test_forward_rejects_mixed_dtypes():
+    m = _op1()
+    g = torch.Generator().manual_seed(3)
+    x, w1, w2, w3, router, accept = (a.cuda() for a in make_moe_inputs(8, 4, 256, 256, g))
+    with pytest.raises(TypeError, match="dtype"):
+        m.tree_moe_forward(x.half(), w1.half(), w2.bfloat16(), w3.half(), router.half(), accept, 2)
+    with pytest.raises(TypeError, match="float16"):
+        m.tree_moe_forward(x, w1, w2, w3, router, accept, 2)
+
+
 ROUTE_CASES = [
     (seed, t, budget, objective, accept_kind)
     for seed, t in ((0, 16), (1, 64), (2, 128), (3, 2048), (4, 4096), (5, 7))

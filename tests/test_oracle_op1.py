@@ -64,6 +64,49 @@ def test_router_logits_are_bf16_rounded_fp64_dot(rng):
     assert np.all(np.abs(logit_gap - exact_gap) <= tol)
 
 
+def test_f16_rounding_matches_numpy():
+    """The oracle's fp32 -> fp16 rounding (fp16 router logits and outputs) is
+    numpy's round-to-nearest-even conversion: random magnitudes over the
+    whole range, subnormals, overflow, and exact halfway cases."""
+    rng = np.random.default_rng(0)
+    mags = 10.0 ** rng.integers(-9, 6, 200000)
+    vals = np.concatenate([
+        (rng.standard_normal(200000) * mags).astype(np.float32),
+        np.array([0.0, -0.0, 65504.0, 65519.996, 65520.0, -65520.0, 1e9, np.inf, -np.inf,
+                  2.0 ** -14, 2.0 ** -24, 2.0 ** -25, 3 * 2.0 ** -26, 2.0 ** -25 * 1.0000001,
+                  1e-30, 6.1e-5, -6.1e-5], np.float32),
+        ((np.arange(1024, 2048, dtype=np.float64) + 0.5) * 2.0 ** -10).astype(np.float32),
+        ((np.arange(1, 1024, dtype=np.float64) + 0.5) * 2.0 ** -24).astype(np.float32),
+    ])
+    got = oracle_c.f32_to_f16_bits(vals)
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    assert np.isnan(oracle_c.f32_to_f16_bits(np.array([np.nan], np.float32)).view(np.float16)[0])
+
+
+def test_router_logits_f16_are_rounded_dot(rng):
+    """fp16 router: each logit is the fp16 rounding of the dot product (within
+    one fp16 ulp of the FP64 value), the gates are the softmax of exactly
+    those logits, and they agree with torch's F.linear on fp16 operands up to
+    one ulp where the fp32 sums round differently."""
+    x = torch.randn(16, 256, generator=rng).to(torch.float16)
+    w = (torch.randn(8, 256, generator=rng) * 0.1).to(torch.float16)
+    bits = oracle_c.router_logits(bf16_bits(x), bf16_bits(w), f16=True)
+    logits = bits.view(np.float16).astype(np.float64)
+    exact = (x.double() @ w.double().t()).numpy()
+    ulp = np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(logits - exact) <= ulp)
+    gates = oracle_c.router_gates(bf16_bits(x), bf16_bits(w), f16=True)
+    ref = torch.softmax(torch.from_numpy(logits).float(), -1).numpy()
+    np.testing.assert_allclose(gates, ref, rtol=2e-6, atol=1e-7)
+    torch_logits = torch.nn.functional.linear(x, w).double().numpy()
+    assert np.all(np.abs(torch_logits - logits) <= ulp)
+    # a planted variant that rounds the same sums to bf16 misses the fp16 bound
+    bf = oracle_c.router_logits(bf16_bits(x), bf16_bits(w)).astype(np.uint32) << 16
+    assert not np.all(np.abs(bf.view(np.float32).astype(np.float64) - exact) <= ulp)
+
+
 def test_router_order_is_64_lane_fold(rng):
     """A planted variant of the reduction order (plain sequential sum) must
     be distinguishable: the oracle's fold is what the device implements."""

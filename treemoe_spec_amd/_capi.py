@@ -20,14 +20,14 @@ F32 = ctypes.c_float
 
 # name -> argtypes; every entry point returns int (0 = ok)
 SIGNATURES: dict[str, list] = {
-    "tm_op1_router_gates": [P, P, I64, I64, I64, P, P],
+    "tm_op1_router_gates": [P, P, I64, I64, I64, P, I32, P],
     "tm_op1_route_bucket": [P, P, I64, I64, I64, F32, I32, I64, I64, I64] + [P] * 10 + [P],
-    "tm_op1_route": [P, P, P, I64, I64, I64, I64, F32, I32, I64, I64, I64] + [P] * 11 + [P],
-    "tm_op1_gemm1": [P, P, P, P, P, P, I64, I64, I64, I64, I64, P],
-    "tm_op1_gemm2": [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
-    "tm_op1_combine": [P, P, P, I64, I64, I64, P],
-    "tm_op1_prefill_gemm1": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P],
-    "tm_op1_prefill_gemm2": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, P],
+    "tm_op1_route": [P, P, P, I64, I64, I64, I64, F32, I32, I64, I64, I64] + [P] * 11 + [I32, P],
+    "tm_op1_gemm1": [P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, P],
+    "tm_op1_gemm2": [P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I32, P],
+    "tm_op1_combine": [P, P, P, I64, I64, I64, I32, P],
+    "tm_op1_prefill_gemm1": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, P],
+    "tm_op1_prefill_gemm2": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I32, P],
     "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, I64, I32, P, P, P, P, P, P],
     "tm_op4_kv_commit": [P, P, I64, I64, I64, I64, I64, I64, I64, P, P, P, I64, P, I64, I64,
                          I64, P, P],
@@ -46,6 +46,7 @@ SIGNATURES: dict[str, list] = {
 TM_OBJECTIVE = {"mass": 0, "critical_path": 1}
 TM_DTYPE_F32 = 0
 TM_DTYPE_BF16 = 1
+TM_DTYPE_F16 = 2
 TM_GEMM_TILE_M = 64
 TM_OP4_MAX_PARTS = 64
 TM_OP4_NOALLOC_MAX_NODES = 2048

@@ -50,9 +50,15 @@ __device__ __forceinline__ u32x4_t ld_b128(__amdgpu_buffer_rsrc_t r, uint32_t of
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
 }
 
+// 16x16x32 MFMA on bf16 or fp16 operands held as 32-bit integer vectors.
+template <int DT>
 __device__ __forceinline__ f32x4_t mfma16(u32x4_t a, u32x4_t b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  if constexpr (DT == TM_DTYPE_F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
 // Keep the machine scheduler from sinking the next chunk's loads below the
@@ -111,7 +117,7 @@ __device__ __forceinline__ f32x4_t reduce_partials(const f32x4_t* red, int nsub,
 
 // ----------------------------------------------------------------- GEMM1 --
 // h[p, n] = bf16( silu(sum_k x[tok(p), k] w1[e, n, k]) * sum_k x[tok(p), k] w3[e, n, k] )
-template <int NSUB>
+template <int NSUB, int DT>
 __device__ __forceinline__ void gemm1_item(uint8_t* lds, const uint16_t* x, const uint16_t* w1,
                                            const uint16_t* w3, uint16_t* __restrict__ hsw,
                                            const int32_t* __restrict__ sorted_slots, int tile,
@@ -171,8 +177,8 @@ __device__ __forceinline__ void gemm1_item(uint8_t* lds, const uint16_t* x, cons
       const u32x4_t f3 = b_frag<NSUB>(scratch + ROWS * C::SROW, lane, s);
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
-        acc1[sub] = mfma16(xf[s * NSUB + sub], f1, acc1[sub]);
-        acc3[sub] = mfma16(xf[s * NSUB + sub], f3, acc3[sub]);
+        acc1[sub] = mfma16<DT>(xf[s * NSUB + sub], f1, acc1[sub]);
+        acc3[sub] = mfma16<DT>(xf[s * NSUB + sub], f3, acc3[sub]);
       }
     }
   };
@@ -217,12 +223,13 @@ __device__ __forceinline__ void gemm1_item(uint8_t* lds, const uint16_t* x, cons
         const float a = s1[i];
         const float b = s3[i];
         const float hv = (a / (1.0f + __expf(-a))) * b;
-        hsw[(frag + (kk >> 3) * 16 + mm) * 8 + (kk & 7)] = tm_f32_to_bf16(hv);
+        hsw[(frag + (kk >> 3) * 16 + mm) * 8 + (kk & 7)] = Half16<DT>::round(hv);
       }
     }
   }
 }
 
+template <int DT>
 __global__ void __launch_bounds__(256, 2)
 tm_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
                 const uint16_t* __restrict__ w3, uint16_t* __restrict__ hsw,
@@ -247,10 +254,10 @@ tm_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
   const int row0 = tiles[4 * tile + 1];
   const int rows = tiles[4 * tile + 2];
   switch ((rows + 15) >> 4) {
-    case 1: gemm1_item<1>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
-    case 2: gemm1_item<2>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
-    case 3: gemm1_item<3>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
-    default: gemm1_item<4>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
+    case 1: gemm1_item<1, DT>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
+    case 2: gemm1_item<2, DT>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
+    case 3: gemm1_item<3, DT>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
+    default: gemm1_item<4, DT>(lds, x, w1, w3, hsw, sorted_slots, tile, ng, e, row0, rows, H, I, x_bytes); break;
   }
 }
 
@@ -259,7 +266,7 @@ tm_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
 // A workgroup streams two 16-row blocks of w2 (32 output columns) that share
 // the h fragments, so each wave keeps as many weight bytes in flight as in
 // the gate/up GEMM.
-template <int NSUB>
+template <int NSUB, int DT>
 __device__ __forceinline__ void gemm2_item(uint8_t* lds, const uint16_t* hsw, const uint16_t* w2,
                                            float* __restrict__ y,
                                            const float* __restrict__ gates_flat,
@@ -320,8 +327,8 @@ __device__ __forceinline__ void gemm2_item(uint8_t* lds, const uint16_t* hsw, co
       const u32x4_t f1 = b_frag<NSUB>(scratch + ROWS * C::SROW, lane, s);
 #pragma unroll
       for (int sub = 0; sub < NSUB; ++sub) {
-        acc0[sub] = mfma16(hf[s * NSUB + sub], f0, acc0[sub]);
-        acc1[sub] = mfma16(hf[s * NSUB + sub], f1, acc1[sub]);
+        acc0[sub] = mfma16<DT>(hf[s * NSUB + sub], f0, acc0[sub]);
+        acc1[sub] = mfma16<DT>(hf[s * NSUB + sub], f1, acc1[sub]);
       }
     }
   };
@@ -367,6 +374,7 @@ __device__ __forceinline__ void gemm2_item(uint8_t* lds, const uint16_t* hsw, co
   }
 }
 
+template <int DT>
 __global__ void __launch_bounds__(256, 2)
 tm_gemm2_kernel(const uint16_t* __restrict__ hsw, const uint16_t* __restrict__ w2,
                 float* __restrict__ y, const float* __restrict__ gates_flat,
@@ -379,10 +387,10 @@ tm_gemm2_kernel(const uint16_t* __restrict__ hsw, const uint16_t* __restrict__ w
   const int row0 = tiles[4 * tile + 1];
   const int rows = tiles[4 * tile + 2];
   switch ((rows + 15) >> 4) {
-    case 1: gemm2_item<1>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
-    case 2: gemm2_item<2>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
-    case 3: gemm2_item<3>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
-    default: gemm2_item<4>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
+    case 1: gemm2_item<1, DT>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
+    case 2: gemm2_item<2, DT>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
+    case 3: gemm2_item<3, DT>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
+    default: gemm2_item<4, DT>(lds, hsw, w2, y, gates_flat, sorted_slots, tile, e, row0, rows, R, H, I, klen, h_bytes); break;
   }
 }
 
@@ -392,6 +400,7 @@ static_assert(kScratchBytes >= WAVES * 4 * 2 * 64 * 16, "gemm1 reduction");
 // --------------------------------------------------------------- combine --
 // out[t, n] = bf16( sum over (k = 0, 1) of sum over split s of y[s, pos(2t+k), n] ),
 // accumulated in exactly that order from 0.
+template <int DT>
 __global__ void __launch_bounds__(256)
 tm_combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ slot_pos,
                   uint16_t* __restrict__ out, int T, int H, int S, int R) {
@@ -410,10 +419,10 @@ tm_combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ slot_
     a0 = a0 + v.x; a1 = a1 + v.y; a2 = a2 + v.z; a3 = a3 + v.w;
   }
   u16x4_t o;
-  o[0] = tm_f32_to_bf16(a0);
-  o[1] = tm_f32_to_bf16(a1);
-  o[2] = tm_f32_to_bf16(a2);
-  o[3] = tm_f32_to_bf16(a3);
+  o[0] = Half16<DT>::round(a0);
+  o[1] = Half16<DT>::round(a1);
+  o[2] = Half16<DT>::round(a2);
+  o[3] = Half16<DT>::round(a3);
   *reinterpret_cast<u16x4_t*>(out + (size_t)t * H + n) = o;
 }
 
@@ -424,17 +433,20 @@ bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 extern "C" int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void* h,
                             const int32_t* sorted_slots, const int32_t* tiles,
                             int64_t max_tiles, int64_t T, int64_t H, int64_t I, int64_t E,
-                            void* stream) {
+                            int dtype, void* stream) {
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS) return TM_ERR_SHAPE;
   if (H < 256 || (H % 256) != 0 || I < 256 || (I % 256) != 0 || max_tiles < 1)
     return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (I * H * 2 >= (int64_t)kOutOfRange || T * H * 2 >= (int64_t)kOutOfRange ||
       max_tiles * MT * I * 2 >= (int64_t)kOutOfRange)
     return TM_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(w1) || !aligned16(w3) || !aligned16(h)) return TM_ERR_ALIGN;
   if ((I / ROWS) * max_tiles > INT32_MAX) return TM_ERR_SHAPE;
   const dim3 grid((unsigned)((I / ROWS) * max_tiles));
-  hipLaunchKernelGGL(tm_gemm1_kernel, grid, dim3(64 * WAVES), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(dtype == TM_DTYPE_F16 ? tm_gemm1_kernel<TM_DTYPE_F16>
+                                           : tm_gemm1_kernel<TM_DTYPE_BF16>,
+                     grid, dim3(64 * WAVES), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)w1, (const uint16_t*)w3,
                      (uint16_t*)h, sorted_slots, tiles, (int)max_tiles, (int)H, (int)I,
                      (uint32_t)(T * H * 2), max_tiles <= 2 * E ? 1 : 0);
@@ -445,8 +457,10 @@ extern "C" int tm_op1_gemm1(const void* x, const void* w1, const void* w3, void*
 extern "C" int tm_op1_gemm2(const void* h, const void* w2, float* y,
                             const float* gates_flat, const int32_t* sorted_slots,
                             const int32_t* tiles, int64_t max_tiles, int64_t split,
-                            int64_t T, int64_t H, int64_t I, int64_t E, void* stream) {
+                            int64_t T, int64_t H, int64_t I, int64_t E, int dtype,
+                            void* stream) {
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS) return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (split < 1 || (I % split) != 0) return TM_ERR_SHAPE;
   const int64_t klen = I / split;
   if (klen < 256 || (klen % 256) != 0 || H < 2 * ROWS || (H % (2 * ROWS)) != 0 ||
@@ -456,7 +470,9 @@ extern "C" int tm_op1_gemm2(const void* h, const void* w2, float* y,
     return TM_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w2)) return TM_ERR_ALIGN;
   const dim3 grid((unsigned)(H / (2 * ROWS)), (unsigned)split, (unsigned)max_tiles);
-  hipLaunchKernelGGL(tm_gemm2_kernel, grid, dim3(64 * WAVES), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(dtype == TM_DTYPE_F16 ? tm_gemm2_kernel<TM_DTYPE_F16>
+                                           : tm_gemm2_kernel<TM_DTYPE_BF16>,
+                     grid, dim3(64 * WAVES), 0, (hipStream_t)stream,
                      (const uint16_t*)h, (const uint16_t*)w2, y, gates_flat, sorted_slots,
                      tiles, (int)(2 * T), (int)H, (int)I, (int)klen,
                      (uint32_t)(max_tiles * MT * I * 2));
@@ -465,11 +481,14 @@ extern "C" int tm_op1_gemm2(const void* h, const void* w2, float* y,
 }
 
 extern "C" int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out, int64_t T,
-                              int64_t H, int64_t split, void* stream) {
+                              int64_t H, int64_t split, int dtype, void* stream) {
   if (T < 1 || T > TM_MAX_TOKENS || H < 4 || (H % 4) != 0 || split < 1) return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (!aligned16(y) || ((uintptr_t)out % 8) != 0) return TM_ERR_ALIGN;
   const dim3 grid((unsigned)T, (unsigned)((H + 1023) / 1024));
-  hipLaunchKernelGGL(tm_combine_kernel, grid, dim3(256), 0, (hipStream_t)stream, y, slot_pos,
+  hipLaunchKernelGGL(dtype == TM_DTYPE_F16 ? tm_combine_kernel<TM_DTYPE_F16>
+                                           : tm_combine_kernel<TM_DTYPE_BF16>,
+                     grid, dim3(256), 0, (hipStream_t)stream, y, slot_pos,
                      (uint16_t*)out, (int)T, (int)H, (int)split, (int)(2 * T));
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;

@@ -82,9 +82,15 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 // 32x32x16 bf16 MFMA.  Lane l: A row l % 32 and B column l % 32, k 8 (l / 32)
 // .. +7; accumulator value v is C[8 (v / 4) + 4 (l / 32) + v % 4][l % 32].
+// (DT: TM_DTYPE_BF16 or TM_DTYPE_F16 operands, same lane layout.)
+template <int DT>
 __device__ __forceinline__ f32x16_t pmfma(u32x4_t a, u32x4_t b, f32x16_t c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  if constexpr (DT == TM_DTYPE_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
 __device__ __forceinline__ int acc_row(int v, int lane) {
@@ -253,7 +259,7 @@ __device__ __forceinline__ u32x4_t frag(const uint8_t* tile, int row, int s, int
 // (<= MT) is the accumulator tiles per wave along the rows: M = MT covers the
 // whole M-tile, M = MT / 2 its first half (a tile with at most BM / 2 real
 // rows, whose other rows are zeros).
-template <class C, int M>
+template <class C, int M, int DT>
 __device__ __forceinline__ void compute_step(const uint8_t* st, const int (&brow)[2],
                                              f32x16_t (&acc)[M][2]) {
   const int lane = threadIdx.x & 63;
@@ -268,7 +274,7 @@ __device__ __forceinline__ void compute_step(const uint8_t* st, const int (&brow
 #pragma unroll
     for (int i = 0; i < M; ++i)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = pmfma(a[i], b[j], acc[i][j]);
+      for (int j = 0; j < 2; ++j) acc[i][j] = pmfma<DT>(a[i], b[j], acc[i][j]);
   }
 }
 
@@ -288,7 +294,7 @@ struct Stages {
 // step k+NS-1 goes into that stage, then step k's MFMAs run.  The barrier
 // waits for this wave's LDS reads only (tm_lds_barrier), not for its
 // outstanding loads: the loads of the next steps stay in flight.
-template <class C, int M>
+template <class C, int M, int DT>
 __device__ __forceinline__ void k_loop(const Stages& sb, const DmaLoad<C>& d, int nk,
                                        const int (&brow)[2], f32x16_t (&acc)[M][2]) {
   constexpr int NS = C::NSTAGE;
@@ -301,7 +307,7 @@ __device__ __forceinline__ void k_loop(const Stages& sb, const DmaLoad<C>& d, in
       wait_vm<(NS - 2) * C::LDS_PER_STEP>();
       tm_lds_barrier();
       dma_step<C>(d, st[(u + NS - 1) % NS], k + u + NS - 1, nk);
-      if (u == 0 || k + u < nk) compute_step<C, M>(st[u], brow, acc);
+      if (u == 0 || k + u < nk) compute_step<C, M, DT>(st[u], brow, acc);
     }
   }
   // the last loads (zeros past the end) must land before the stages are reused
@@ -322,7 +328,7 @@ __device__ __forceinline__ uint8_t* h_stage(const Stages& sb, int m) {
 // The MFMAs and the epilogue of one gate/up tile with M accumulator tiles
 // per wave (see compute_step): SwiGLU in registers, the bf16 tile staged in
 // LDS, then a coalesced store of its `rows` rows.
-template <class C, int M>
+template <class C, int M, int DT>
 __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d, int nk,
                                            int rows, int p0, int n0, int I,
                                            uint16_t* __restrict__ h) {
@@ -338,7 +344,7 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   // accumulator column blocks: j = 0 -> w1 rows 32 wn ..; j = 1 -> the same w3 rows
   const int brow[2] = {32 * wn, PBN / 2 + 32 * wn};
-  k_loop<C, M>(sb, d, nk, brow, acc);
+  k_loop<C, M, DT>(sb, d, nk, brow, acc);
 #pragma unroll
   for (int i = 0; i < M; ++i)
 #pragma unroll
@@ -348,7 +354,7 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
       const float hv = (a / (1.0f + __expf(-a))) * b;
       const int m = 32 * M * wm + 32 * i + acc_row(v, lane);
       const int c = 32 * wn + (lane & 31);
-      *reinterpret_cast<uint16_t*>(h_stage<C>(sb, m) + c * 2) = tm_f32_to_bf16(hv);
+      *reinterpret_cast<uint16_t*>(h_stage<C>(sb, m) + c * 2) = Half16<DT>::round(hv);
     }
   __syncthreads();
 #pragma unroll
@@ -362,7 +368,7 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
   }
 }
 
-template <class C>
+template <class C, int DT>
 __global__ void __launch_bounds__(NT)
 tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
                         const uint16_t* __restrict__ w3, uint16_t* __restrict__ h,
@@ -404,11 +410,11 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   // MFMAs; its A rows past `rows` are loaded as zeros without memory traffic
   if constexpr (C::MT > 1) {
     if (rows <= C::PBM / 2) {
-      gemm1_tile<C, C::MT / 2>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+      gemm1_tile<C, C::MT / 2, DT>(sb, d, H / C::PBK, rows, p0, n0, I, h);
       return;
     }
   }
-  gemm1_tile<C, C::MT>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+  gemm1_tile<C, C::MT, DT>(sb, d, H / C::PBK, rows, p0, n0, I, h);
 }
 
 // ---------------------------------------------------------------- down --
@@ -416,7 +422,7 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 // for the rows p of one M-tile and 256 output columns n.  The fp32 partials
 // go straight from the accumulators: for each accumulator value, 32 lanes
 // store 128 contiguous bytes of one row.
-template <class C, int M>
+template <class C, int M, int DT>
 __device__ __forceinline__ void gemm2_tile(const Stages& sb, const DmaLoad<C>& d, int nk,
                                            int rows, int p0, int H,
                                            const float* __restrict__ gates_flat,
@@ -432,7 +438,7 @@ __device__ __forceinline__ void gemm2_tile(const Stages& sb, const DmaLoad<C>& d
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   const int brow[2] = {64 * wn, 64 * wn + 32};
-  k_loop<C, M>(sb, d, nk, brow, acc);
+  k_loop<C, M, DT>(sb, d, nk, brow, acc);
 #pragma unroll
   for (int i = 0; i < M; ++i)
 #pragma unroll
@@ -449,7 +455,7 @@ __device__ __forceinline__ void gemm2_tile(const Stages& sb, const DmaLoad<C>& d
     }
 }
 
-template <class C>
+template <class C, int DT>
 __global__ void __launch_bounds__(NT)
 tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restrict__ w2,
                         float* __restrict__ y, const float* __restrict__ gates_flat,
@@ -491,21 +497,22 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   float* ys = y + (size_t)seg * R * H + n0;
   if constexpr (C::MT > 1) {
     if (rows <= C::PBM / 2) {  // as in gate/up
-      gemm2_tile<C, C::MT / 2>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots, ys);
+      gemm2_tile<C, C::MT / 2, DT>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots,
+                                   ys);
       return;
     }
   }
-  gemm2_tile<C, C::MT>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots, ys);
+  gemm2_tile<C, C::MT, DT>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots, ys);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
-template <class C>
+template <class C, int DT>
 void launch_gemm1(const void* x, const void* w1, const void* w3, void* h,
                   const int32_t* sorted_slots, const int32_t* expert_offsets,
                   const int32_t* tiles, int64_t max_tiles, int64_t T, int64_t H, int64_t I,
                   int64_t E, int64_t mt_max, int64_t jobs, hipStream_t stream) {
-  hipLaunchKernelGGL(tm_prefill_gemm1_kernel<C>, dim3((unsigned)jobs), dim3(NT), 0, stream,
+  hipLaunchKernelGGL((tm_prefill_gemm1_kernel<C, DT>), dim3((unsigned)jobs), dim3(NT), 0, stream,
                      (const uint16_t*)x, (const uint16_t*)w1, (const uint16_t*)w3,
                      (uint16_t*)h, sorted_slots, expert_offsets, tiles, (int)max_tiles,
                      (int)E, (int)H, (int)I, (int)mt_max, (uint32_t)(T * H * 2));
@@ -516,9 +523,10 @@ void launch_gemm1(const void* x, const void* w1, const void* w3, void* h,
 extern "C" int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w3, void* h,
                                     const int32_t* sorted_slots, const int32_t* expert_offsets,
                                     const int32_t* tiles, int64_t max_tiles, int64_t T,
-                                    int64_t H, int64_t I, int64_t E, void* stream) {
+                                    int64_t H, int64_t I, int64_t E, int dtype, void* stream) {
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS || max_tiles < 1)
     return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (H < Tile128::PBK || (H % Tile128::PBK) != 0 || I < PBN / 2 || (I % (PBN / 2)) != 0)
     return TM_ERR_SHAPE;
   if (I * H * 2 >= (int64_t)kOOR || T * H * 2 >= (int64_t)kOOR || 2 * T * I * 2 >= (int64_t)kOOR)
@@ -532,12 +540,19 @@ extern "C" int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w
       max_tiles, big ? mtile_bound<Tile256>(2 * T, E) : mtile_bound<Tile128>(2 * T, E));
   const int64_t jobs = launch_jobs(mt_max, I / (PBN / 2));
   if (jobs > INT32_MAX) return TM_ERR_SHAPE;
-  if (big) {
-    launch_gemm1<Tile256>(x, w1, w3, h, sorted_slots, expert_offsets, tiles, max_tiles, T, H, I,
-                          E, mt_max, jobs, (hipStream_t)stream);
+  const hipStream_t st = (hipStream_t)stream;
+  if (big && dtype == TM_DTYPE_F16) {
+    launch_gemm1<Tile256, TM_DTYPE_F16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
+                                        max_tiles, T, H, I, E, mt_max, jobs, st);
+  } else if (big) {
+    launch_gemm1<Tile256, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
+                                         max_tiles, T, H, I, E, mt_max, jobs, st);
+  } else if (dtype == TM_DTYPE_F16) {
+    launch_gemm1<Tile128, TM_DTYPE_F16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
+                                        max_tiles, T, H, I, E, mt_max, jobs, st);
   } else {
-    launch_gemm1<Tile128>(x, w1, w3, h, sorted_slots, expert_offsets, tiles, max_tiles, T, H, I,
-                          E, mt_max, jobs, (hipStream_t)stream);
+    launch_gemm1<Tile128, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
+                                         max_tiles, T, H, I, E, mt_max, jobs, st);
   }
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
@@ -547,10 +562,11 @@ extern "C" int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y,
                                     const float* gates_flat, const int32_t* sorted_slots,
                                     const int32_t* expert_offsets, const int32_t* tiles,
                                     int64_t max_tiles, int64_t split, int64_t T, int64_t H,
-                                    int64_t I, int64_t E, void* stream) {
+                                    int64_t I, int64_t E, int dtype, void* stream) {
   using C = Tile128;
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS || max_tiles < 1)
     return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (split < 1 || (I % split) != 0) return TM_ERR_SHAPE;
   const int64_t klen = I / split;
   if (klen < C::PBK || (klen % C::PBK) != 0 || H < PBN || (H % PBN) != 0) return TM_ERR_SHAPE;
@@ -559,7 +575,9 @@ extern "C" int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y,
   const int64_t mt_max = std::min<int64_t>(max_tiles, mtile_bound<C>(2 * T, E));
   const int64_t jobs = launch_jobs(mt_max, (H / PBN) * split);
   if (jobs > INT32_MAX) return TM_ERR_SHAPE;
-  hipLaunchKernelGGL(tm_prefill_gemm2_kernel<C>, dim3((unsigned)jobs), dim3(NT), 0,
+  hipLaunchKernelGGL((dtype == TM_DTYPE_F16 ? tm_prefill_gemm2_kernel<C, TM_DTYPE_F16>
+                                            : tm_prefill_gemm2_kernel<C, TM_DTYPE_BF16>),
+                     dim3((unsigned)jobs), dim3(NT), 0,
                      (hipStream_t)stream, (const uint16_t*)h, (const uint16_t*)w2, y, gates_flat,
                      sorted_slots, expert_offsets, tiles, (int)max_tiles, (int)E, (int)(2 * T),
                      (int)H, (int)I, (int)klen, (int)split, (int)mt_max,

@@ -31,18 +31,28 @@ constexpr int kMaxPaddedRows = 16384;
 // 13.1 us at H = 4096, E = 8).
 constexpr int kRowsMinTokens = 1024;
 
-__device__ __forceinline__ float lo_bf16(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float hi_bf16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+// The two 16-bit elements of a 32-bit word, widened exactly to fp32 (DT is
+// TM_DTYPE_BF16 or TM_DTYPE_F16).
+template <int DT>
+__device__ __forceinline__ float lo16(uint32_t w) {
+  return DT == TM_DTYPE_F16 ? tm_f16_to_f32((uint16_t)(w & 0xffffu)) : __uint_as_float(w << 16);
+}
+template <int DT>
+__device__ __forceinline__ float hi16(uint32_t w) {
+  return DT == TM_DTYPE_F16 ? tm_f16_to_f32((uint16_t)(w >> 16))
+                            : __uint_as_float(w & 0xffff0000u);
+}
 
+template <int DT>
 __device__ __forceinline__ float fma8(uint4 xv, uint4 wv, float acc) {
-  acc = fmaf(lo_bf16(xv.x), lo_bf16(wv.x), acc);
-  acc = fmaf(hi_bf16(xv.x), hi_bf16(wv.x), acc);
-  acc = fmaf(lo_bf16(xv.y), lo_bf16(wv.y), acc);
-  acc = fmaf(hi_bf16(xv.y), hi_bf16(wv.y), acc);
-  acc = fmaf(lo_bf16(xv.z), lo_bf16(wv.z), acc);
-  acc = fmaf(hi_bf16(xv.z), hi_bf16(wv.z), acc);
-  acc = fmaf(lo_bf16(xv.w), lo_bf16(wv.w), acc);
-  acc = fmaf(hi_bf16(xv.w), hi_bf16(wv.w), acc);
+  acc = fmaf(lo16<DT>(xv.x), lo16<DT>(wv.x), acc);
+  acc = fmaf(hi16<DT>(xv.x), hi16<DT>(wv.x), acc);
+  acc = fmaf(lo16<DT>(xv.y), lo16<DT>(wv.y), acc);
+  acc = fmaf(hi16<DT>(xv.y), hi16<DT>(wv.y), acc);
+  acc = fmaf(lo16<DT>(xv.z), lo16<DT>(wv.z), acc);
+  acc = fmaf(hi16<DT>(xv.z), hi16<DT>(wv.z), acc);
+  acc = fmaf(lo16<DT>(xv.w), lo16<DT>(wv.w), acc);
+  acc = fmaf(hi16<DT>(xv.w), hi16<DT>(wv.w), acc);
   return acc;
 }
 
@@ -62,10 +72,11 @@ __device__ __forceinline__ void router_softmax(const float* s_logit, float* __re
 
 // Router for token t in one workgroup.  Logit (t, e): lane l of the wave that
 // owns expert e accumulates the 8-element chunks l, l+64, ... in element order
-// (fmaf of exact bf16 products); the 64 lane sums are combined by a halving
-// tree (xor butterfly) and rounded to bf16, as F.linear on bf16 operands
-// returns (treemoe/kernels/op1_tree_moe.py:676).  Softmax (:677) in fp32: max,
+// (fmaf of exact products of the 16-bit inputs); the 64 lane sums are combined
+// by a halving tree (xor butterfly) and rounded to the input type (bf16 or
+// fp16), as F.linear on such operands returns (treemoe/kernels/op1_tree_moe.py:676).  Softmax (:677) in fp32: max,
 // e^(l - max), a sum in expert order, a correctly rounded division.
+template <int DT>
 __device__ __forceinline__ void router_token(const uint16_t* __restrict__ x,
                                              const uint16_t* __restrict__ wg,
                                              float* __restrict__ gates, int t, int H, int E,
@@ -86,12 +97,12 @@ __device__ __forceinline__ void router_token(const uint16_t* __restrict__ x,
         wv[u] = wr[c + 64 * u];
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) acc = fma8(xv[u], wv[u], acc);
+      for (int u = 0; u < 8; ++u) acc = fma8<DT>(xv[u], wv[u], acc);
     }
-    for (; c < nchunk; c += 64) acc = fma8(xr[c], wr[c], acc);
+    for (; c < nchunk; c += 64) acc = fma8<DT>(xr[c], wr[c], acc);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
-    if (lane == 0) s_logit[e] = tm_bf16_to_f32(tm_f32_to_bf16(acc));
+    if (lane == 0) s_logit[e] = Half16<DT>::to_f32(Half16<DT>::round(acc));
   }
   __syncthreads();
   if (wave == 0) router_softmax(s_logit, gates, t, E, lane);
@@ -400,11 +411,12 @@ __device__ void bucket_all(const BucketArgs& a, BucketShared& sh) {
   }
 }
 
+template <int DT>
 __global__ void __launch_bounds__(kThreads)
 tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
                  float* __restrict__ gates, int T, int H, int E) {
   __shared__ float s_logit[TM_MAX_EXPERTS];
-  router_token(x, wg, gates, blockIdx.x, H, E, s_logit);
+  router_token<DT>(x, wg, gates, blockIdx.x, H, E, s_logit);
 }
 
 // Router for many tokens: wave w of workgroup b takes token kWaves b + w and
@@ -415,7 +427,7 @@ tm_router_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg
 // gates are bit-identical to it.
 constexpr int kRowsLdsChunks = 4096;  // W_g staged in LDS: E * H / 8 <= 4096 (64 KB)
 
-template <int XC>
+template <int DT, int XC>
 __global__ void __launch_bounds__(kThreads)
 tm_router_rows_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ wg,
                       float* __restrict__ gates, int T, int H, int E) {
@@ -436,10 +448,10 @@ tm_router_rows_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict
     const uint4* wr = s_w + e * nchunk;
     float acc = 0.0f;
 #pragma unroll
-    for (int u = 0; u < XC; ++u) acc = fma8(xv[u], wr[lane + 64 * u], acc);
+    for (int u = 0; u < XC; ++u) acc = fma8<DT>(xv[u], wr[lane + 64 * u], acc);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off);
-    if (lane == 0) s_logit[wave][e] = tm_bf16_to_f32(tm_f32_to_bf16(acc));
+    if (lane == 0) s_logit[wave][e] = Half16<DT>::to_f32(Half16<DT>::round(acc));
   }
   // s_logit[wave] is written and read by this wave only: its LDS operations
   // complete in order
@@ -449,20 +461,29 @@ tm_router_rows_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict
 // Launch the router: the row kernel when W_g fits its LDS copy, H is one of
 // its register shapes and there are enough tokens to fill the chip with
 // workgroups of kWaves tokens; otherwise one workgroup per token.
-void launch_router(const uint16_t* x, const uint16_t* wg, float* gates, int T, int H, int E,
-                   hipStream_t stream) {
+template <int DT>
+void launch_router_dt(const uint16_t* x, const uint16_t* wg, float* gates, int T, int H, int E,
+                      hipStream_t stream) {
   const bool rows_ok = T >= kRowsMinTokens && E * (H / 8) <= kRowsLdsChunks;
   const dim3 rgrid((unsigned)((T + kWaves - 1) / kWaves));
   if (rows_ok && H == 2048) {
-    hipLaunchKernelGGL(tm_router_rows_kernel<4>, rgrid, dim3(kThreads), 0, stream, x, wg, gates,
-                       T, H, E);
+    hipLaunchKernelGGL((tm_router_rows_kernel<DT, 4>), rgrid, dim3(kThreads), 0, stream, x, wg,
+                       gates, T, H, E);
   } else if (rows_ok && H == 4096) {
-    hipLaunchKernelGGL(tm_router_rows_kernel<8>, rgrid, dim3(kThreads), 0, stream, x, wg, gates,
-                       T, H, E);
+    hipLaunchKernelGGL((tm_router_rows_kernel<DT, 8>), rgrid, dim3(kThreads), 0, stream, x, wg,
+                       gates, T, H, E);
   } else {
-    hipLaunchKernelGGL(tm_router_kernel, dim3((unsigned)T), dim3(kThreads), 0, stream, x, wg,
+    hipLaunchKernelGGL(tm_router_kernel<DT>, dim3((unsigned)T), dim3(kThreads), 0, stream, x, wg,
                        gates, T, H, E);
   }
+}
+
+void launch_router(const uint16_t* x, const uint16_t* wg, float* gates, int T, int H, int E,
+                   int dtype, hipStream_t stream) {
+  if (dtype == TM_DTYPE_F16)
+    launch_router_dt<TM_DTYPE_F16>(x, wg, gates, T, H, E, stream);
+  else
+    launch_router_dt<TM_DTYPE_BF16>(x, wg, gates, T, H, E, stream);
 }
 
 __global__ void __launch_bounds__(kThreads) tm_bucket_kernel(BucketArgs args) {
@@ -730,11 +751,12 @@ BucketArgs make_args(const float* gates, const float* accept, int64_t T, int64_t
 }  // namespace
 
 extern "C" int tm_op1_router_gates(const void* x, const void* wg, int64_t T, int64_t H,
-                                   int64_t E, float* gates, void* stream) {
+                                   int64_t E, float* gates, int dtype, void* stream) {
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS || H < 8 || (H % 8) != 0)
     return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (((uintptr_t)x % 16) != 0 || ((uintptr_t)wg % 16) != 0) return TM_ERR_ALIGN;
-  launch_router((const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E,
+  launch_router((const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E, dtype,
                 (hipStream_t)stream);
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
@@ -766,16 +788,17 @@ extern "C" int tm_op1_route(const void* x, const void* wg, const float* accept, 
                             int64_t* padded_slots, int64_t* block_expert_ids,
                             int64_t* slot_to_row, float* demand, int32_t* expert_offsets,
                             int32_t* sorted_slots, int32_t* slot_pos, int32_t* tiles,
-                            void* stream) {
+                            int dtype, void* stream) {
   const int rc = check_bucket_args(T, E, budget, objective, block_m, max_blocks, max_tiles);
   if (rc != TM_OK) return rc;
   if (H < 8 || (H % 8) != 0) return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (((uintptr_t)x % 16) != 0 || ((uintptr_t)wg % 16) != 0) return TM_ERR_ALIGN;
   const BucketArgs a = make_args(gates, accept, T, E, budget, tau, objective, block_m, max_blocks,
                                  max_tiles, topk_ids, gates_flat, padded_slots,
                                  block_expert_ids, slot_to_row, demand, expert_offsets,
                                  sorted_slots, slot_pos, tiles);
-  launch_router((const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E,
+  launch_router((const uint16_t*)x, (const uint16_t*)wg, gates, (int)T, (int)H, (int)E, dtype,
                 (hipStream_t)stream);
   TM_HIP_CHECK_LAUNCH();
   launch_bucket(a, (hipStream_t)stream);

@@ -7,6 +7,7 @@
 #include "../../include/treemoe_amd.h"
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
 
@@ -28,6 +29,29 @@ __device__ __forceinline__ uint16_t tm_f32_to_bf16(float f) {
   u += 0x7fffu + ((u >> 16) & 1u);
   return (uint16_t)(u >> 16);
 }
+
+__device__ __forceinline__ float tm_f16_to_f32(uint16_t u) {
+  return (float)__builtin_bit_cast(_Float16, u);
+}
+
+// fp32 -> fp16, round to nearest even (the hardware conversion: subnormals
+// kept, overflow to infinity, NaN stays NaN), as torch's float->half.
+__device__ __forceinline__ uint16_t tm_f32_to_f16(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// 16-bit element type of op1's activations and weights: TM_DTYPE_BF16 or
+// TM_DTYPE_F16.  to_f32 widens one element exactly; round narrows an fp32
+// value to the type with round-to-nearest-even.
+template <int DT>
+struct Half16 {
+  static __device__ __forceinline__ float to_f32(uint16_t u) {
+    return DT == TM_DTYPE_F16 ? tm_f16_to_f32(u) : tm_bf16_to_f32(u);
+  }
+  static __device__ __forceinline__ uint16_t round(float f) {
+    return DT == TM_DTYPE_F16 ? tm_f32_to_f16(f) : tm_f32_to_bf16(f);
+  }
+};
 
 // Wait for this wave's LDS operations, then a plain workgroup barrier.  Unlike
 // __syncthreads() this does not drain outstanding global loads, so weight

@@ -109,11 +109,20 @@ def _require_device(*tensors: torch.Tensor) -> None:
                 "(no CPU fallback is provided)")
 
 
-def _require_bf16(name: str, t: torch.Tensor) -> None:
-    if t.dtype != torch.bfloat16:
-        raise TypeError(f"{name} must be torch.bfloat16, got {t.dtype}")
+_DTYPE_CODE = {torch.bfloat16: _capi.TM_DTYPE_BF16, torch.float16: _capi.TM_DTYPE_F16}
+
+
+def _require_half(name: str, t: torch.Tensor, like: torch.Tensor | None = None) -> int:
+    """The C-ABI dtype code of a contiguous bf16 or fp16 tensor (the
+    reference kernels take either, op1_tree_moe.py:762-766); ``like`` fixes
+    the dtype all operands must share."""
+    if t.dtype not in _DTYPE_CODE:
+        raise TypeError(f"{name} must be torch.bfloat16 or torch.float16, got {t.dtype}")
+    if like is not None and t.dtype != like.dtype:
+        raise TypeError(f"{name} must have x's dtype {like.dtype}, got {t.dtype}")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
+    return _DTYPE_CODE[t.dtype]
 
 
 class _Workspace:
@@ -159,7 +168,7 @@ def _workspace(n: int, e: int, hidden: int, inter: int, x: torch.Tensor) -> _Wor
 def _launch_router(x: torch.Tensor, router_weight: torch.Tensor, gates: torch.Tensor) -> None:
     n, hidden = x.shape
     call("tm_op1_router_gates", ptr(x), ptr(router_weight), n, hidden,
-         router_weight.shape[0], ptr(gates), _capi.stream_of(x.device))
+         router_weight.shape[0], ptr(gates), _DTYPE_CODE[x.dtype], _capi.stream_of(x.device))
 
 
 def _launch_route_bucket(gates, accept, n, e, budget, tau, objective, block_m, max_blocks,
@@ -179,7 +188,7 @@ def _launch_route(x, router_weight, accept, budget, tau, objective, block_m, max
          router_weight.shape[0], budget, float(tau), TM_OBJECTIVE[objective], block_m,
          max_blocks, max_tiles, ptr(gates), ptr(topk), ptr(gates_flat), ptr(padded), ptr(blk),
          ptr(s2r), ptr(demand), ptr(offsets), ptr(sorted_slots), ptr(slot_pos), ptr(tiles),
-         _capi.stream_of(x.device))
+         _DTYPE_CODE[x.dtype], _capi.stream_of(x.device))
 
 
 def _prep_accept(node_accept_prob: torch.Tensor, n: int) -> torch.Tensor:
@@ -227,8 +236,8 @@ def route_and_bucket(
     slot_pos = torch.empty(2 * n, dtype=i32, device=dev)
     tiles = torch.empty(max_tiles, 4, dtype=i32, device=dev)
     if router_gates is None:
-        _require_bf16("x", x)
-        _require_bf16("router_weight", router_weight)
+        _require_half("x", x)
+        _require_half("router_weight", router_weight, like=x)
         gates = torch.empty(n, e, dtype=torch.float32, device=dev)
         _launch_route(x, router_weight, accept, expert_budget, top1_threshold,
                       routing_objective, block_m, max_blocks, max_tiles, gates, topk, gflat,
@@ -328,8 +337,8 @@ def route_experts(
     workspace)."""
     _check_budget(expert_budget, router_weight.shape[0], routing_objective)
     _require_device(x, router_weight, node_accept_prob)
-    _require_bf16("x", x)
-    _require_bf16("router_weight", router_weight)
+    _require_half("x", x)
+    _require_half("router_weight", router_weight, like=x)
     n, hidden = x.shape
     e = router_weight.shape[0]
     if router_weight.shape[1] != hidden:
@@ -372,8 +381,9 @@ def tree_moe_forward(
     precomputed phase-1 handle from route_experts(); None routes inline."""
     _check_budget(expert_budget, router_weight.shape[0], routing_objective)
     _require_device(x, w1, w2, w3, router_weight, node_accept_prob)
-    for name, t in (("x", x), ("w1", w1), ("w2", w2), ("w3", w3)):
-        _require_bf16(name, t)
+    dt = _require_half("x", x)
+    for name, t in (("w1", w1), ("w2", w2), ("w3", w3), ("router_weight", router_weight)):
+        _require_half(name, t, like=x)
     n, hidden = x.shape
     e, inter, h_w = w1.shape
     if h_w != hidden or w3.shape != w1.shape or tuple(w2.shape) != (e, hidden, inter):
@@ -386,7 +396,8 @@ def tree_moe_forward(
     ws = routing.ws
     if (routing.topk_ids.shape[0] != n or ws.partial.shape[1] != 2 * n
             or ws.h.shape != (ws.max_tiles * TILE_M, inter) or ws.partial.shape[2] != hidden
-            or ws.num_experts != e or routing.max_tiles > ws.max_tiles):
+            or ws.num_experts != e or routing.max_tiles > ws.max_tiles
+            or ws.h.dtype != x.dtype):
         raise ValueError("routing was computed for a different shape")
     stream = _capi.stream_of(x.device)
     split = ws.split
@@ -394,16 +405,16 @@ def tree_moe_forward(
         split = _tiled_split(n, expert_budget, e, hidden, inter, ws)
         call("tm_op1_prefill_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h),
              ptr(routing.sorted_slots), ptr(routing.expert_offsets), ptr(routing.tiles),
-             routing.max_tiles, n, hidden, inter, e, stream)
+             routing.max_tiles, n, hidden, inter, e, dt, stream)
         call("tm_op1_prefill_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial),
              ptr(routing.gates_flat), ptr(routing.sorted_slots), ptr(routing.expert_offsets),
-             ptr(routing.tiles), routing.max_tiles, split, n, hidden, inter, e, stream)
+             ptr(routing.tiles), routing.max_tiles, split, n, hidden, inter, e, dt, stream)
     else:
         call("tm_op1_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h), ptr(routing.sorted_slots),
-             ptr(routing.tiles), routing.max_tiles, n, hidden, inter, e, stream)
+             ptr(routing.tiles), routing.max_tiles, n, hidden, inter, e, dt, stream)
         call("tm_op1_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial), ptr(routing.gates_flat),
              ptr(routing.sorted_slots), ptr(routing.tiles), routing.max_tiles, ws.split, n,
-             hidden, inter, e, stream)
+             hidden, inter, e, dt, stream)
     if out is not None:
         if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
             raise ValueError("out must be a contiguous tensor like x")
@@ -411,5 +422,5 @@ def tree_moe_forward(
     else:
         result = torch.empty_like(x)
     call("tm_op1_combine", ptr(ws.partial), ptr(routing.slot_pos), ptr(result), n, hidden,
-         split, stream)
+         split, dt, stream)
     return result
