@@ -1,13 +1,15 @@
 """End to end on the GPU: greedy speculative decoding through this build's
 tree attention, op1 MoE (via the engine hook) and op4 verify + KV commit
-equals greedy AR decoding (the reference's lossless red line,
+equals greedy AR decoding token for token (the reference's lossless red line,
 tests/test_spec_lossless.py:58-84, 312-372, at B = 8).
 
 The reference runs that gate in float32 with a torch MoE.  Here attention and
 the MoE are bf16 kernels, and a 15-node verification forward sums its keys in
-a different order than a one-node AR forward, so the two can differ in the
-last bits; a mismatch is accepted only at an AR step whose top-2 logit margin
-is below NEAR_TIE (logits are ~N(0, 1)), and decoding must agree up to there.
+a different order than a one-node AR forward, so the two could differ in the
+last bits of a logit; only an AR step whose top-2 logit margin is that small
+could then decode differently.  Every kernel is bitwise deterministic and the
+inputs are seeded, so each case below has one outcome: the test requires the
+token sequences to be identical and reports the smallest AR margin it met.
 """
 
 from __future__ import annotations
@@ -20,14 +22,12 @@ from tests.engine_harness import (TinyConfig, TinyEngine, ar_generate, random_mo
 
 pytestmark = pytest.mark.gpu
 
-NEAR_TIE = 0.02
-
 
 def _say(msg: str) -> None:
     print(msg, flush=True)
 
 
-@pytest.mark.parametrize("seed", [1, 7, 42])
+@pytest.mark.parametrize("seed", [1, 7, 42, 3, 11, 2024])
 def test_spec_decode_matches_ar(seed):
     _say(f"engine spec vs AR seed={seed}")
     cfg = TinyConfig()
@@ -37,10 +37,8 @@ def test_spec_decode_matches_ar(seed):
     ar, margins = ar_generate(TinyEngine(cfg, model), prompt, 40)
     eng = TinyEngine(cfg, model)
     spec, steps, accepted = spec_generate(eng, prompt, 40, ar, seed)
-    mismatch = next((i for i, (a, b) in enumerate(zip(ar, spec)) if a != b), None)
-    _say(f"  steps={steps} accepted={accepted} first mismatch={mismatch}")
-    if mismatch is not None:
-        assert margins[mismatch] < NEAR_TIE, (mismatch, margins[mismatch], ar, spec)
+    _say(f"  steps={steps} accepted={accepted} smallest AR top-2 margin={min(margins):.4f}")
+    assert spec == ar, (next(i for i, (a, b) in enumerate(zip(ar, spec)) if a != b), ar, spec)
     # the planted paths were accepted: fewer steps than tokens; the cache holds
     # the prompt but its last token, then [root] + accepted path per step (the
     # last bonus token is the next root, not yet committed)
