@@ -103,15 +103,24 @@ def test_structured_masks(n, seq_len):
             assert torch.equal(out.cpu(), want), name
 
 
-def test_write_tree_and_nothing_else():
-    _say("tree attention write_tree bytes")
+@pytest.mark.parametrize("n,seq_len,chunk_keys", [
+    (40, 333, 0),
+    (200, 333, 64),    # tree rows spread over four chunks, chunk start inside a page
+    (130, 0, 64),      # no prefix: every chunk holds tree rows only
+])
+def test_write_tree_and_nothing_else(n, seq_len, chunk_keys):
+    """Each tree row is stored once to its scratch slot by the chunk that
+    holds it, whatever the chunking; nothing else in the cache changes."""
+    _say(f"tree attention write_tree bytes n={n} seq={seq_len} chunk={chunk_keys}")
     from treemoe_spec_amd.kernels.tree_attention import tree_attention
 
-    n, page = 40, 16
-    kv, q, k, v, mask = _case(n, 16, 4, 333, page, 7)
+    page = 16
+    kv, q, k, v, mask = _case(n, 16, 4, seq_len, page, 7)
     k0, v0 = kv.k.clone(), kv.v.clone()
-    tree_attention(q.cuda(), k.cuda(), v.cuda(), kv, 0, mask.cuda())
+    out = tree_attention(q.cuda(), k.cuda(), v.cuda(), kv, 0, mask.cuda(),
+                         chunk_keys=chunk_keys)
     torch.cuda.synchronize()
+    _check(out, _oracle(kv, q, k, v, mask, 0))
     kk, vv = k0.clone(), v0.clone()
     for j in range(n):
         pg, off = kv.tree_pages[j // page], j % page
@@ -121,7 +130,8 @@ def test_write_tree_and_nothing_else():
     # write_tree=False leaves the cache alone
     kv.k.copy_(k0)
     kv.v.copy_(v0)
-    tree_attention(q.cuda(), k.cuda(), v.cuda(), kv, 0, mask.cuda(), write_tree=False)
+    tree_attention(q.cuda(), k.cuda(), v.cuda(), kv, 0, mask.cuda(), write_tree=False,
+                   chunk_keys=chunk_keys)
     torch.cuda.synchronize()
     assert torch.equal(kv.k, k0) and torch.equal(kv.v, v0)
 

@@ -144,6 +144,46 @@ __device__ __forceinline__ void store_stage(uint8_t* buf, int quad, int part, co
   }
 }
 
+// Tree rows among a staged stage's keys (keys seq_len .. c1-1) into the
+// scratch pages: tree node j lives in page s_tpages[j / page] at slot j % page.
+__device__ __forceinline__ void store_tree_rows(const AttnParams& p, const int* s_tpages, int kb,
+                                                int c1, int quad, int64_t head_off,
+                                                const Stage& st) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int key = kb + 4 * quad + r;
+    if (key >= p.seq_len && key < c1) {
+      const int node = key - p.seq_len;
+      const int64_t dst = (int64_t)s_tpages[node >> p.page_shift] * p.stride_page +
+                          (int64_t)(node & ((1 << p.page_shift) - 1)) * p.stride_slot +
+                          head_off;
+      *reinterpret_cast<u32x4_t*>(p.k_cache + dst) = st.k[r];
+      *reinterpret_cast<u32x4_t*>(p.v_cache + dst) = st.v[r];
+    }
+  }
+}
+
+// Visibility of keys kb .. kb+63 for one query, bit i for key kb + i:
+// prefix keys (key < seq_len) visible, tree key seq_len + j visible when bit j
+// of the query's mask row mw is set, keys at or past the chunk end c1 hidden.
+// d = kb - seq_len (> -64 for a stage that is not all prefix), e = c1 - kb.
+__device__ __forceinline__ uint64_t stage_window(const uint64_t mw[4], int d, int e) {
+  uint64_t win;
+  if (d >= 0) {
+    const int w = d >> 6, sh = d & 63;
+    uint64_t a = mw[0], b = mw[1];
+    if (w == 1) { a = mw[1]; b = mw[2]; }
+    if (w == 2) { a = mw[2]; b = mw[3]; }
+    if (w >= 3) { a = mw[3]; b = 0; }
+    win = sh ? (a >> sh) | (b << (64 - sh)) : a;
+  } else {
+    const int pre = -d;
+    win = pre >= 64 ? ~0ull : (mw[0] << pre) | ((1ull << pre) - 1);
+  }
+  if (e < 64) win &= (1ull << e) - 1;
+  return win;
+}
+
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 
@@ -152,6 +192,100 @@ typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// One 64-key stage of one wave against its 32 queries: keys kb .. kb+63 from
+// the LDS stage at kl (K rows, then V^T), scores masked on boundary stages,
+// the online softmax state (m_run, l_run) and O^T (acc) updated.
+__device__ __forceinline__ void attend_stage(const AttnParams& p, const uint8_t* kl, int kb,
+                                             int c1, const uint64_t mw[4], int half, int c32,
+                                             const u32x4_t qf[kHD / 16], f32x16_t acc[kHD / 32],
+                                             float& m_run, float& l_run) {
+  const uint8_t* vl = kl + kKBytes;
+  // S^T = K Q^T over two 32-key tiles; lane holds keys
+  // 32 kt + 8 (v/4) + 4 half + v%4 of query c32 in sc[kt][v]
+  f32x16_t sc[2];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) sc[kt][v] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < kHD / 16; ++ks) {
+      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(
+          kl + (32 * kt + c32) * kKStride + ks * 32 + half * 16);
+      sc[kt] = mfma32(a, qf[ks], sc[kt]);
+    }
+  }
+  // tree and chunk-end masking (boundary stages only); integer and/or, so
+  // the visibility is a plain select
+  if (!(kb + kKeys <= min(c1, p.seq_len))) {
+    // key kb + 32 kt + 8 (v/4) + 4 half + v%4 is bit 8 (v/4) + v%4 of
+    // dword kt of the lane's window shifted by 4 half
+    const uint64_t win = stage_window(mw, kb - p.seq_len, c1 - kb) >> (4 * half);
+    const uint32_t wd[2] = {(uint32_t)win, (uint32_t)(win >> 32)};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const uint32_t bit = (wd[kt] >> (8 * (v >> 2) + (v & 3))) & 1u;
+        sc[kt][v] = bit ? sc[kt][v] : -INFINITY;
+      }
+    }
+  }
+  // running max in base 2 (scale > 0 commutes with max); the query's other
+  // 32 keys of the stage sit in lane c32 ^ 32
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[kt][v]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float cand = mx * p.scale_log2;
+  // The reference point moves only when the stage maximum exceeds it by more
+  // than 2^8 (weights stay <= 256), so the accumulators are rescaled rarely;
+  // the final division by the sum taken against the same reference makes
+  // this exact in real arithmetic.
+  const bool bump = cand > m_run + 8.0f;
+  if (__any(bump)) {
+    const float m_use = bump ? cand : m_run;
+    const float alpha = bump ? exp2f(m_run - m_use) : 1.0f;
+#pragma unroll
+    for (int ht = 0; ht < kHD / 32; ++ht) acc[ht] *= alpha;
+    l_run *= alpha;
+    m_run = m_use;
+  }
+  const float neg_base = m_run == -INFINITY ? 0.0f : -m_run;
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float e = __builtin_amdgcn_exp2f(fmaf(sc[kt][v], p.scale_log2, neg_base));
+      sc[kt][v] = e;
+      l_run += e;
+    }
+  }
+  // O^T += V^T P^T: k-step (kt, m) covers keys 32 kt + 16 m + [0, 16); its
+  // k slot j of lane half h is key 32 kt + 16 m + 8 (j/4) + 4 h + j%4, which
+  // is the lane's own value sc[kt][8 m + j]
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      u32x4_t b;
+      b.x = pack_bf16(sc[kt][8 * m + 0], sc[kt][8 * m + 1]);
+      b.y = pack_bf16(sc[kt][8 * m + 2], sc[kt][8 * m + 3]);
+      b.z = pack_bf16(sc[kt][8 * m + 4], sc[kt][8 * m + 5]);
+      b.w = pack_bf16(sc[kt][8 * m + 6], sc[kt][8 * m + 7]);
+#pragma unroll
+      for (int ht = 0; ht < kHD / 32; ++ht) {
+        const uint8_t* vr = vl + (32 * ht + c32) * kVStride + (32 * kt + 16 * m + 4 * half) * 2;
+        const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
+        const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 16);
+        const u32x4_t a = {lo.x, lo.y, hi.x, hi.y};
+        acc[ht] = mfma32(a, b, acc[ht]);
+      }
+    }
+  }
 }
 
 // Partials of one (workgroup slot, wave): 16 groups x 64 lanes x 4 fp16 of
@@ -166,6 +300,7 @@ constexpr int kStatFloats = 64;                      // 32 queries x (m, l)
 __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_buf[2 * kStage];
   __shared__ int s_pages[kMaxPages];
+  __shared__ int s_tpages[kMaxNodes / 4];
 
   const int x8 = blockIdx.x & 7, y = blockIdx.x >> 3;
   const int rb = y % p.row_blocks;
@@ -182,26 +317,19 @@ __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p)
   const int part = (tid >> 2) & 15;
   const int64_t head_off = (int64_t)kvhead * kHD + part * 8;
 
-  // tree rows of this KV head into the scratch pages (one workgroup per head)
-  if (p.write_tree && rb == 0 && chunk == p.chunks - 1) {
-    for (int u = tid; u < p.n * 16; u += kThreads) {
-      const int node = u >> 4, pc = u & 15;
-      const int64_t src = (int64_t)node * p.tail_stride + kvhead * kHD + pc * 8;
-      const int64_t dst = (int64_t)p.scratch_pages[node >> p.page_shift] * p.stride_page +
-                          (int64_t)(node & ((1 << p.page_shift) - 1)) * p.stride_slot +
-                          kvhead * kHD + pc * 8;
-      *reinterpret_cast<u32x4_t*>(p.k_cache + dst) =
-          *reinterpret_cast<const u32x4_t*>(p.k_tail + src);
-      *reinterpret_cast<u32x4_t*>(p.v_cache + dst) =
-          *reinterpret_cast<const u32x4_t*>(p.v_tail + src);
-    }
-  }
-
-  // block-table entries of the chunk's prefix keys
+  // block-table entries of the chunk's prefix keys; the workgroups of row
+  // block 0 also store the chunk's tree rows of this KV head into the scratch
+  // pages, from the registers that stage them (each tree row lies in exactly
+  // one chunk), so they need the scratch page list
   const int pre_end = min(c1, p.seq_len);
   const int npages = pre_end > c0 ? ((pre_end - 1) >> p.page_shift) - (c0 >> p.page_shift) + 1 : 0;
   for (int i = tid; i < npages; i += kThreads)
     s_pages[i] = p.block_table[(c0 >> p.page_shift) + i];
+  const bool write_rows = p.write_tree && rb == 0 && c1 > p.seq_len;
+  if (write_rows) {
+    const int tpages = ((p.n - 1) >> p.page_shift) + 1;
+    for (int i = tid; i < tpages; i += kThreads) s_tpages[i] = p.scratch_pages[i];
+  }
 
   // this lane's query (column c32 of the wave's 32): Q^T fragments, mask row
   const int row = rb * kRows + wave * 32 + c32;
@@ -228,6 +356,8 @@ __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p)
 
   Stage st;
   load_stage(p, s_pages, c0, c0, c1, head_off, quad, st);
+  if (write_rows && c0 + kKeys > p.seq_len)
+    store_tree_rows(p, s_tpages, c0, c1, quad, head_off, st);
   store_stage(s_buf, quad, part, st);
   __syncthreads();
 
@@ -238,105 +368,20 @@ __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p)
     for (int v = 0; v < 16; ++v) acc[ht][v] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
+  // stage s in LDS buffer s & 1; the next stage's loads go out before this
+  // stage's MFMAs and land in the other buffer after them
   const int nstage = (c1 - c0 + kKeys - 1) / kKeys;
   for (int s = 0; s < nstage; ++s) {
-    const int kb = c0 + s * kKeys;
-    // next stage's loads go out before this stage's MFMAs (the last stage
-    // reloads itself: unconditional, so the wait counts stay exact)
-    const int kn = c0 + min(s + 1, nstage - 1) * kKeys;
-    load_stage(p, s_pages, kn, c0, c1, head_off, quad, st);
-
-    const uint8_t* kl = s_buf + (s & 1) * kStage;
-    const uint8_t* vl = kl + kKBytes;
-    // S^T = K Q^T over two 32-key tiles; lane holds keys
-    // 32 kt + 8 (v/4) + 4 half + v%4 of query c32 in sc[kt][v]
-    f32x16_t sc[2];
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) sc[kt][v] = 0.0f;
-#pragma unroll
-      for (int ks = 0; ks < kHD / 16; ++ks) {
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(
-            kl + (32 * kt + c32) * kKStride + ks * 32 + half * 16);
-        sc[kt] = mfma32(a, qf[ks], sc[kt]);
-      }
+    const int kb = c0 + s * kKeys, kn = kb + kKeys;
+    const bool more = s + 1 < nstage;
+    if (more) load_stage(p, s_pages, kn, c0, c1, head_off, quad, st);
+    attend_stage(p, s_buf + (s & 1) * kStage, kb, c1, mw, half, c32, qf, acc, m_run, l_run);
+    if (more) {
+      if (write_rows && kn + kKeys > p.seq_len)
+        store_tree_rows(p, s_tpages, kn, c1, quad, head_off, st);
+      store_stage(s_buf + ((s + 1) & 1) * kStage, quad, part, st);
+      __syncthreads();
     }
-    // tree and chunk-end masking (boundary stages only); integer and/or, so
-    // the visibility is a plain select
-    if (!(kb + kKeys <= min(c1, p.seq_len))) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = kb + 32 * kt + 8 * (v >> 2) + 4 * half + (v & 3);
-          const int j = key - p.seq_len;
-          uint64_t word = mw[0];
-          word = j >= 64 ? mw[1] : word;
-          word = j >= 128 ? mw[2] : word;
-          word = j >= 192 ? mw[3] : word;
-          const uint32_t bit = (uint32_t)(word >> (j & 63)) & 1u;
-          const uint32_t vis = (uint32_t)(key < c1) & ((uint32_t)(j < 0) | bit);
-          sc[kt][v] = vis ? sc[kt][v] : -INFINITY;
-        }
-      }
-    }
-    // running max in base 2 (scale > 0 commutes with max); the query's other
-    // 32 keys of the stage sit in lane c32 ^ 32
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[kt][v]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float cand = mx * p.scale_log2;
-    // The reference point moves only when the stage maximum exceeds it by more
-    // than 2^8 (weights stay <= 256), so the accumulators are rescaled rarely;
-    // the final division by the sum taken against the same reference makes
-    // this exact in real arithmetic.
-    const bool bump = cand > m_run + 8.0f;
-    if (__any(bump)) {
-      const float m_use = bump ? cand : m_run;
-      const float alpha = bump ? exp2f(m_run - m_use) : 1.0f;
-#pragma unroll
-      for (int ht = 0; ht < kHD / 32; ++ht) acc[ht] *= alpha;
-      l_run *= alpha;
-      m_run = m_use;
-    }
-    const float neg_base = m_run == -INFINITY ? 0.0f : -m_run;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float e = __builtin_amdgcn_exp2f(fmaf(sc[kt][v], p.scale_log2, neg_base));
-        sc[kt][v] = e;
-        l_run += e;
-      }
-    }
-    // O^T += V^T P^T: k-step (kt, m) covers keys 32 kt + 16 m + [0, 16); its
-    // k slot j of lane half h is key 32 kt + 16 m + 8 (j/4) + 4 h + j%4, which
-    // is the lane's own value sc[kt][8 m + j]
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        u32x4_t b;
-        b.x = pack_bf16(sc[kt][8 * m + 0], sc[kt][8 * m + 1]);
-        b.y = pack_bf16(sc[kt][8 * m + 2], sc[kt][8 * m + 3]);
-        b.z = pack_bf16(sc[kt][8 * m + 4], sc[kt][8 * m + 5]);
-        b.w = pack_bf16(sc[kt][8 * m + 6], sc[kt][8 * m + 7]);
-#pragma unroll
-        for (int ht = 0; ht < kHD / 32; ++ht) {
-          const uint8_t* vr = vl + (32 * ht + c32) * kVStride + (32 * kt + 16 * m + 4 * half) * 2;
-          const u32x2_t lo = *reinterpret_cast<const u32x2_t*>(vr);
-          const u32x2_t hi = *reinterpret_cast<const u32x2_t*>(vr + 16);
-          const u32x4_t a = {lo.x, lo.y, hi.x, hi.y};
-          acc[ht] = mfma32(a, b, acc[ht]);
-        }
-      }
-    }
-    store_stage(s_buf + ((s + 1) & 1) * kStage, quad, part, st);
-    __syncthreads();
   }
 
   // the two lanes of a query hold partial sums over disjoint keys
