@@ -97,6 +97,21 @@ def test_tree_attention_plan():
     assert chunks.value == 65 and ws.value == 65 * 8 * 2 * 4 * (32 * 128 * 2 + 32 * 2 * 4)
     assert plan(64, 32, 8, 128, 4096, 16, 0, ctypes.byref(chunks), ctypes.byref(ws)) == 0
     assert 8 * 2 * chunks.value >= 200   # automatic chunks spread over the 256 CUs
+    # prefix and tree keys chunk separately: 4096 = 12 x 320 + 256 prefix
+    # keys, then the tree keys (64 or 256) in one chunk of their own; a
+    # 300-key prefix at 64 keys per chunk takes 5 chunks, the tree one more
+    assert plan(64, 32, 8, 128, 4096, 16, 320, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    assert chunks.value == 13 + 1
+    assert plan(256, 8, 8, 128, 4096, 16, 320, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    assert chunks.value == 13 + 1
+    assert plan(64, 32, 8, 128, 300, 16, 64, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    assert chunks.value == 5 + 1
+    # work that fits one chunk stays one chunk (no combine)
+    assert plan(64, 32, 8, 128, 100, 16, 256, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    assert chunks.value == 1 and ws.value == 0
+    # no prefix: tree keys only, in chunks of 64
+    assert plan(130, 8, 2, 128, 0, 16, 64, ctypes.byref(chunks), ctypes.byref(ws)) == 0
+    assert chunks.value == 3
     assert plan(64, 32, 8, 64, 4096, 16, 0, ctypes.byref(chunks), ctypes.byref(ws)) == 1001
 
 

@@ -53,6 +53,15 @@ struct Half16 {
   }
 };
 
+// 8-byte store at device scope (relaxed): written through this XCD's L2
+// rather than left dirty in it.  For data a later kernel reads, this spares the
+// end-of-kernel release, which has to write every dirty L2 line back before
+// the next kernel starts (the 8 XCD L2s are not coherent with each other).
+__device__ __forceinline__ void tm_store_through(void* ptr, uint64_t bits) {
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(ptr), bits, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Wait for this wave's LDS operations, then a plain workgroup barrier.  Unlike
 // __syncthreads() this does not drain outstanding global loads, so weight
 // prefetches stay in flight across the barrier.

@@ -11,6 +11,9 @@
 // chunk is staged through LDS 64 keys at a time and each key byte is read from
 // HBM once per (KV head, chunk), by the row blocks of that pair, which are
 // launched on one XCD (launch indices congruent mod 8) so they share its L2.
+// When the keys take several chunks, the prefix and the tree keys are chunked
+// separately: the tree chunk's masked stage and its tree-row stores then run
+// beside the prefix chunks instead of lengthening one of them.
 //
 // Per wave and 64-key stage (v_mfma_f32_32x32x16_bf16 throughout):
 //   S^T = K Q^T    A = K rows from LDS, B = Q^T held in registers, two 32-key
@@ -23,8 +26,8 @@
 //                  4(l/32) + j%4, the lane's own value 8m + j; A = V^T read with
 //                  the same key map from a transposed copy of V in LDS.
 // A chunk's normalised O^T (fp16), reference maximum and sum go to a workspace
-// and a second kernel combines the chunks in chunk order (deterministic); with
-// one chunk the first kernel writes the output itself.
+// (written through L2) and a second kernel combines the chunks in chunk order
+// (deterministic); with one chunk the first kernel writes the output itself.
 #include <algorithm>
 #include <cmath>
 
@@ -43,8 +46,8 @@ constexpr int kVBytes = kHD * kVStride;     // 17,408
 constexpr int kStage = kKBytes + kVBytes;   // 34,816
 constexpr int kMaxPages = 512;              // block-table entries staged per chunk
 constexpr int kMaxNodes = 256;              // tree nodes (mask words per row <= 4)
-constexpr int kTargetGroups = 512;          // workgroups the planner aims for
-constexpr int kMinChunk = 256;              // keys per chunk, lower bound
+constexpr int kCUs = 256;                   // MI355X compute units
+constexpr int kMaxAutoLen = 16384;          // longest chunk the planner considers
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
@@ -63,6 +66,7 @@ struct AttnParams {
   float* stats;
   int64_t q_stride, tail_stride, out_stride, stride_page, stride_slot;
   int page_shift, seq_len, n, hq, kvh, group, rows, row_blocks, chunks, chunk_len, pairs;
+  int pre_chunks, split;      // chunks < pre_chunks tile keys [0, split), the rest [split, end)
   int mask_words, write_tree;
   float scale_log2;
 };
@@ -311,8 +315,9 @@ __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p)
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, c32 = lane & 31;
   const int s_total = p.seq_len + p.n;
-  const int c0 = chunk * p.chunk_len;
-  const int c1 = min(c0 + p.chunk_len, s_total);
+  const bool lead = chunk < p.pre_chunks;
+  const int c0 = (lead ? 0 : p.split) + (lead ? chunk : chunk - p.pre_chunks) * p.chunk_len;
+  const int c1 = min(c0 + p.chunk_len, lead ? p.split : s_total);
   const int quad = (tid & 3) + 4 * (tid >> 6);
   const int part = (tid >> 2) & 15;
   const int64_t head_off = (int64_t)kvhead * kHD + part * 8;
@@ -404,7 +409,8 @@ __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p)
     }
     return;
   }
-  // chunk partial: O^T / l in fp16 (|value| <= max |v|), and (m, l)
+  // chunk partial: O^T / l in fp16 (|value| <= max |v|), and (m, l), written
+  // through L2 for the combine kernel
   const int64_t slot = ((int64_t)(kvhead * p.row_blocks + rb) * p.chunks + chunk) * 4 + wave;
   _Float16* pp = reinterpret_cast<_Float16*>(p.part) + slot * kPartHalves + lane * 4;
 #pragma unroll
@@ -416,12 +422,12 @@ __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p)
       h[1] = (_Float16)(acc[ht][4 * gq + 1] * inv);
       h[2] = (_Float16)(acc[ht][4 * gq + 2] * inv);
       h[3] = (_Float16)(acc[ht][4 * gq + 3] * inv);
-      *reinterpret_cast<f16x4_t*>(pp + (ht * 4 + gq) * 256) = h;
+      tm_store_through(pp + (ht * 4 + gq) * 256, __builtin_bit_cast(uint64_t, h));
     }
   }
   if (half == 0) {
     f32x2_t st2 = {m_run, l_run};
-    *reinterpret_cast<f32x2_t*>(p.stats + slot * kStatFloats + c32 * 2) = st2;
+    tm_store_through(p.stats + slot * kStatFloats + c32 * 2, __builtin_bit_cast(uint64_t, st2));
   }
 }
 
@@ -488,31 +494,95 @@ __global__ void tm_tree_mask_pack_kernel(const uint8_t* __restrict__ mask, int n
 
 struct Plan {
   int64_t row_blocks, chunks, chunk_len, pairs, groups, part_floats, stats_floats;
+  int64_t pre_chunks, split;
 };
+
+// Chunking of keys 0 .. seq_len+n-1 into chunks of at most len keys.  The
+// prefix and the tree keys are chunked separately, so that the tree's masked
+// stage (and its tree-row stores) runs beside the prefix chunks rather than
+// lengthening one of them; the prefix chunks are evened out to whole stages.
+// Work that fits one chunk stays one chunk (no combine).
+struct Split {
+  int64_t len, pre_chunks, split, chunks;
+};
+
+Split split_keys(int64_t seq_len, int64_t n, int64_t len) {
+  const int64_t s_total = seq_len + n;
+  Split sp;
+  sp.len = len;
+  const int64_t whole = (s_total + len - 1) / len;
+  if (whole > 1 && seq_len > 0) {
+    const int64_t pre = (seq_len + len - 1) / len;
+    sp.len = ((seq_len + pre - 1) / pre + kKeys - 1) / kKeys * kKeys;
+    sp.pre_chunks = (seq_len + sp.len - 1) / sp.len;
+    sp.split = seq_len;
+    sp.chunks = sp.pre_chunks + (n + sp.len - 1) / sp.len;
+  } else {
+    sp.pre_chunks = whole;
+    sp.split = s_total;
+    sp.chunks = whole;
+  }
+  return sp;
+}
+
+int64_t groups_of(int64_t kvh, int64_t row_blocks, int64_t chunks) {
+  return (kvh * chunks + 7) / 8 * 8 * row_blocks;
+}
+
+// Planner cost of a split, in units of one 64-key stage of one workgroup:
+// the longest chunk's stages plus ~2 stages of workgroup prologue and
+// epilogue, times 1.6 per extra workgroup a CU has to hold (co-resident
+// workgroups share its SIMDs), plus, with several chunks, ~2 stages for the
+// combine kernel's launch and 0.1 per chunk it merges (its loop over the
+// chunks).  Fitted to measurements on MI355X at 1024 .. 16384 cached positions
+// (N = 64, 32 query and 8 KV heads), where it picks the fastest chunk length
+// of those tried.
+double split_cost(const Split& sp, int64_t s_total, int64_t kvh, int64_t row_blocks) {
+  const int64_t keys = sp.chunks > 1 ? sp.len : s_total;
+  const double stages = (double)((keys + kKeys - 1) / kKeys);
+  const int64_t groups = groups_of(kvh, row_blocks, sp.chunks);
+  const double stretch = groups <= kCUs ? 1.0 : 0.8 * (double)((groups + kCUs - 1) / kCUs);
+  const double combine = sp.chunks > 1 ? 2.0 + 0.1 * (double)sp.chunks : 0.0;
+  return (stages + 2.0) * stretch + combine;
+}
 
 int make_plan(int64_t n, int64_t hq, int64_t kvh, int64_t seq_len, int64_t page_size,
               int64_t chunk_keys, Plan* pl) {
   const int64_t s_total = seq_len + n;
   const int64_t rows = (hq / kvh) * n;
   pl->row_blocks = (rows + kRows - 1) / kRows;
-  const int64_t base = kvh * pl->row_blocks;
-  int64_t len;
-  if (chunk_keys > 0) {
-    len = chunk_keys;
-  } else {
-    int64_t chunks = (kTargetGroups + base - 1) / base;
-    chunks = std::min<int64_t>(chunks, std::max<int64_t>(1, s_total / kMinChunk));
-    len = (s_total + chunks - 1) / chunks;
-  }
-  len = (len + kKeys - 1) / kKeys * kKeys;
   // the chunk's block-table entries must fit the LDS copy
   const int64_t max_len = (int64_t)(kMaxPages - 2) * page_size / kKeys * kKeys;
   if (max_len < kKeys) return TM_ERR_SHAPE;
-  len = std::min(len, max_len);
-  pl->chunk_len = len;
-  pl->chunks = (s_total + len - 1) / len;
+  Split sp;
+  if (chunk_keys > 0) {
+    const int64_t len = std::min((chunk_keys + kKeys - 1) / kKeys * kKeys, max_len);
+    sp = split_keys(seq_len, n, len);
+  } else {
+    // every distinct chunk length from the longest allowed down to one stage
+    const int64_t top = std::min<int64_t>(max_len, kMaxAutoLen);
+    const int64_t keys = seq_len > 0 ? seq_len : s_total;
+    sp = split_keys(seq_len, n, std::min((s_total + kKeys - 1) / kKeys * kKeys, top));
+    double best = split_cost(sp, s_total, kvh, pl->row_blocks);
+    int64_t parts = (keys + top - 1) / top;
+    for (;;) {
+      const int64_t len = ((keys + parts - 1) / parts + kKeys - 1) / kKeys * kKeys;
+      const Split c = split_keys(seq_len, n, len);
+      const double cost = split_cost(c, s_total, kvh, pl->row_blocks);
+      if (cost < best) {
+        best = cost;
+        sp = c;
+      }
+      if (len <= kKeys) break;
+      parts = (keys + len - kKeys - 1) / (len - kKeys);  // first count giving a shorter len
+    }
+  }
+  pl->chunk_len = sp.len;
+  pl->pre_chunks = sp.pre_chunks;
+  pl->split = sp.split;
+  pl->chunks = sp.chunks;
   pl->pairs = kvh * pl->chunks;
-  pl->groups = (pl->pairs + 7) / 8 * 8 * pl->row_blocks;
+  pl->groups = groups_of(kvh, pl->row_blocks, pl->chunks);
   const int64_t slots = pl->chunks > 1 ? kvh * pl->row_blocks * pl->chunks * 4 : 0;
   pl->part_floats = slots * kPartHalves / 2;  // fp16 partials, counted in floats
   pl->stats_floats = slots * kStatFloats;
@@ -617,6 +687,8 @@ extern "C" int tm_tree_attention(const void* q, int64_t q_stride, const void* k_
   p.row_blocks = (int)pl.row_blocks;
   p.chunks = (int)pl.chunks;
   p.chunk_len = (int)pl.chunk_len;
+  p.pre_chunks = (int)pl.pre_chunks;
+  p.split = (int)pl.split;
   p.pairs = (int)pl.pairs;
   p.mask_words = (int)((N + 63) / 64);
   p.write_tree = write_tree ? 1 : 0;
