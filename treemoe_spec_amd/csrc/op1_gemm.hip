@@ -30,7 +30,6 @@ constexpr uint32_t kOutOfRange = 0x80000000u;
 constexpr int kNt = 2;             // buffer cache policy: non-temporal
 constexpr int kScratchBytes = 69632;  // >= 4 waves x 2 matrices x 16 rows x 528 B
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 template <int NSUB>
 struct Cfg {

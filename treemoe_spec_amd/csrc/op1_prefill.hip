@@ -70,7 +70,6 @@ struct Tile {
 using Tile128 = Tile<128, 64, 3>;
 using Tile256 = Tile<256, 32, 4>;
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t pbuf(const void* base, uint32_t bytes) {

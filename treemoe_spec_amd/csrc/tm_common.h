@@ -10,6 +10,7 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint16_t u16x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 #define TM_HIP_CHECK_LAUNCH()                                   \
   do {                                                          \
@@ -53,13 +54,24 @@ struct Half16 {
   }
 };
 
-// 8-byte store at device scope (relaxed): written through this XCD's L2
-// rather than left dirty in it.  For data a later kernel reads, this spares the
-// end-of-kernel release, which has to write every dirty L2 line back before
-// the next kernel starts (the 8 XCD L2s are not coherent with each other).
-__device__ __forceinline__ void tm_store_through(void* ptr, uint64_t bits) {
-  __hip_atomic_store(reinterpret_cast<uint64_t*>(ptr), bits, __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
+// Store at device scope (relaxed; 2, 4 or 8 bytes): written through this
+// XCD's L2 rather than left dirty in it.  For data a later kernel reads, this
+// spares the end-of-kernel release, which has to write every dirty L2 line
+// back before the next kernel starts (the 8 XCD L2s are not coherent with
+// each other).
+template <typename T>
+__device__ __forceinline__ void tm_store_through(T* ptr, T v) {
+  static_assert(sizeof(T) == 2 || sizeof(T) == 4 || sizeof(T) == 8, "2, 4 or 8 bytes");
+  if constexpr (sizeof(T) == 2) {
+    __hip_atomic_store(reinterpret_cast<uint16_t*>(ptr), __builtin_bit_cast(uint16_t, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else if constexpr (sizeof(T) == 4) {
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(ptr), __builtin_bit_cast(uint32_t, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(ptr), __builtin_bit_cast(uint64_t, v),
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // Wait for this wave's LDS operations, then a plain workgroup barrier.  Unlike

@@ -49,7 +49,6 @@ constexpr int kMaxNodes = 256;              // tree nodes (mask words per row <=
 constexpr int kCUs = 256;                   // MI355X compute units
 constexpr int kMaxAutoLen = 16384;          // longest chunk the planner considers
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 struct AttnParams {
@@ -422,12 +421,12 @@ __global__ void __launch_bounds__(kThreads, 2) tm_tree_attn_kernel(AttnParams p)
       h[1] = (_Float16)(acc[ht][4 * gq + 1] * inv);
       h[2] = (_Float16)(acc[ht][4 * gq + 2] * inv);
       h[3] = (_Float16)(acc[ht][4 * gq + 3] * inv);
-      tm_store_through(pp + (ht * 4 + gq) * 256, __builtin_bit_cast(uint64_t, h));
+      tm_store_through(reinterpret_cast<f16x4_t*>(pp + (ht * 4 + gq) * 256), h);
     }
   }
   if (half == 0) {
     f32x2_t st2 = {m_run, l_run};
-    tm_store_through(p.stats + slot * kStatFloats + c32 * 2, __builtin_bit_cast(uint64_t, st2));
+    tm_store_through(reinterpret_cast<f32x2_t*>(p.stats + slot * kStatFloats + c32 * 2), st2);
   }
 }
 
