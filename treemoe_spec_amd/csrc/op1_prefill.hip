@@ -60,6 +60,10 @@ struct Tile {
   static constexpr int BLD = BBYTES / (NT * 16);  //                                   B
   static constexpr int LDS_PER_STEP = ALD + BLD;
   static constexpr int MT = PBM / 64;             // 32-row accumulator tiles per wave
+  // weight loads of an expert with a single M-tile go non-temporal (below)
+  // for tiles of at most 128 rows; the 256-row gate/up tile runs where most
+  // experts take several M-tiles, and there the policy measured slower
+  static constexpr bool NT_WEIGHTS = BM <= 128;
   // h rows staged per stage: the whole tile in one stage when it fits
   static constexpr int HROWS = PBM * HSTRIDE <= STAGE ? PBM : PBM / NSTAGE;
   static_assert(ALD >= 1 && BLD >= 1 && BLD % 2 == 0 && CPR >= 4, "tile shape");
@@ -163,7 +167,8 @@ int64_t launch_jobs(int64_t mt_max, int64_t ncol) {
 template <class C>
 __device__ __forceinline__ bool find_mtile(const int32_t* __restrict__ offsets,
                                            const int32_t* __restrict__ tiles, int max_tiles,
-                                           int E, int idx, int* e, int* p0, int* rows) {
+                                           int E, int idx, int* e, int* p0, int* rows,
+                                           bool* single) {
   int acc = 0, tile64 = 0;
   for (int k = 0; k < E; ++k) {
     const int o = offsets[k];
@@ -175,6 +180,7 @@ __device__ __forceinline__ bool find_mtile(const int32_t* __restrict__ offsets,
       *e = k;
       *p0 = o + m0;
       *rows = min(C::PBM, cnt - m0);
+      *single = nt == 1;
       return true;
     }
     acc += nt;
@@ -223,8 +229,13 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, uint8_t* ld
                                            uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voffset, 0, 0, 0);
 }
+// The same with the non-temporal cache policy (weights streamed through).
+__device__ __forceinline__ void lds_load16_nt(__amdgpu_buffer_rsrc_t r, uint8_t* lds,
+                                              uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voffset, 0, 0, 2);
+}
 
-template <class C>
+template <class C, bool NTB>
 __device__ __forceinline__ void dma_step(const DmaLoad<C>& d, uint8_t* st, int kstep, int nk) {
   const uint32_t kb = (uint32_t)kstep * (uint32_t)C::PROW;
   const bool valid = kstep < nk;
@@ -235,8 +246,12 @@ __device__ __forceinline__ void dma_step(const DmaLoad<C>& d, uint8_t* st, int k
                (valid && d.aoff[i] != kOOR) ? d.aoff[i] + kb : kOOR);
 #pragma unroll
   for (int i = 0; i < C::BLD; ++i)
-    lds_load16(i < C::BLD / 2 ? d.rb0 : d.rb1, st + C::ABYTES + (8 * i + w) * 1024,
-               valid ? d.boff[i] + kb : kOOR);
+    if constexpr (NTB)
+      lds_load16_nt(i < C::BLD / 2 ? d.rb0 : d.rb1, st + C::ABYTES + (8 * i + w) * 1024,
+                    valid ? d.boff[i] + kb : kOOR);
+    else
+      lds_load16(i < C::BLD / 2 ? d.rb0 : d.rb1, st + C::ABYTES + (8 * i + w) * 1024,
+                 valid ? d.boff[i] + kb : kOOR);
 }
 
 // Wait until at most n of this thread's vector-memory operations are
@@ -293,19 +308,19 @@ struct Stages {
 // step k+NS-1 goes into that stage, then step k's MFMAs run.  The barrier
 // waits for this wave's LDS reads only (tm_lds_barrier), not for its
 // outstanding loads: the loads of the next steps stay in flight.
-template <class C, int M, int DT>
+template <class C, int M, int DT, bool NTB>
 __device__ __forceinline__ void k_loop(const Stages& sb, const DmaLoad<C>& d, int nk,
                                        const int (&brow)[2], f32x16_t (&acc)[M][2]) {
   constexpr int NS = C::NSTAGE;
   uint8_t* const st[4] = {sb.s0, sb.s1, sb.s2, sb.s3};
 #pragma unroll
-  for (int u = 0; u < NS - 1; ++u) dma_step<C>(d, st[u], u, nk);
+  for (int u = 0; u < NS - 1; ++u) dma_step<C, NTB>(d, st[u], u, nk);
   for (int k = 0; k < nk; k += NS) {
 #pragma unroll
     for (int u = 0; u < NS; ++u) {
       wait_vm<(NS - 2) * C::LDS_PER_STEP>();
       tm_lds_barrier();
-      dma_step<C>(d, st[(u + NS - 1) % NS], k + u + NS - 1, nk);
+      dma_step<C, NTB>(d, st[(u + NS - 1) % NS], k + u + NS - 1, nk);
       if (u == 0 || k + u < nk) compute_step<C, M, DT>(st[u], brow, acc);
     }
   }
@@ -327,7 +342,7 @@ __device__ __forceinline__ uint8_t* h_stage(const Stages& sb, int m) {
 // The MFMAs and the epilogue of one gate/up tile with M accumulator tiles
 // per wave (see compute_step): SwiGLU in registers, the bf16 tile staged in
 // LDS, then a coalesced store of its `rows` rows.
-template <class C, int M, int DT>
+template <class C, int M, int DT, bool NTB>
 __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d, int nk,
                                            int rows, int p0, int n0, int I,
                                            uint16_t* __restrict__ h) {
@@ -343,7 +358,7 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   // accumulator column blocks: j = 0 -> w1 rows 32 wn ..; j = 1 -> the same w3 rows
   const int brow[2] = {32 * wn, PBN / 2 + 32 * wn};
-  k_loop<C, M, DT>(sb, d, nk, brow, acc);
+  k_loop<C, M, DT, NTB>(sb, d, nk, brow, acc);
 #pragma unroll
   for (int i = 0; i < M; ++i)
 #pragma unroll
@@ -384,7 +399,8 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   const int n_mt = min(count_mtiles<C>(offsets, E), mt_max);
   if (!job_of((int)blockIdx.x, n_mt, ncol, &mt, &cb)) return;
   int e, p0, rows;
-  if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows)) return;
+  bool single;
+  if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows, &single)) return;
   const int n0 = cb * (PBN / 2);  // first h column of the block
 
   DmaLoad<C> d;
@@ -407,13 +423,21 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   }
   // a tile with at most BM / 2 real rows (an expert's last) runs half the
   // MFMAs; its A rows past `rows` are loaded as zeros without memory traffic
+  // An expert that takes one M-tile has its weights read by this job alone:
+  // they stream through with the non-temporal policy (a load-only probe
+  // streams 7.1 TB/s with it, 6.2 without).  With several M-tiles the other
+  // jobs of the expert find them in L2, so those loads stay cached.
   if constexpr (C::MT > 1) {
     if (rows <= C::PBM / 2) {
-      gemm1_tile<C, C::MT / 2, DT>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+      if (C::NT_WEIGHTS && single)
+        gemm1_tile<C, C::MT / 2, DT, C::NT_WEIGHTS>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+      else gemm1_tile<C, C::MT / 2, DT, false>(sb, d, H / C::PBK, rows, p0, n0, I, h);
       return;
     }
   }
-  gemm1_tile<C, C::MT, DT>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+  if (C::NT_WEIGHTS && single)
+    gemm1_tile<C, C::MT, DT, C::NT_WEIGHTS>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+  else gemm1_tile<C, C::MT, DT, false>(sb, d, H / C::PBK, rows, p0, n0, I, h);
 }
 
 // ---------------------------------------------------------------- down --
@@ -421,7 +445,7 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 // for the rows p of one M-tile and 256 output columns n.  The fp32 partials
 // go straight from the accumulators: for each accumulator value, 32 lanes
 // store 128 contiguous bytes of one row.
-template <class C, int M, int DT>
+template <class C, int M, int DT, bool NTB>
 __device__ __forceinline__ void gemm2_tile(const Stages& sb, const DmaLoad<C>& d, int nk,
                                            int rows, int p0, int H,
                                            const float* __restrict__ gates_flat,
@@ -437,7 +461,7 @@ __device__ __forceinline__ void gemm2_tile(const Stages& sb, const DmaLoad<C>& d
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   const int brow[2] = {64 * wn, 64 * wn + 32};
-  k_loop<C, M, DT>(sb, d, nk, brow, acc);
+  k_loop<C, M, DT, NTB>(sb, d, nk, brow, acc);
 #pragma unroll
   for (int i = 0; i < M; ++i)
 #pragma unroll
@@ -473,7 +497,8 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   const int cb = job / nsplit;
   const int seg = job - cb * nsplit;
   int e, p0, rows;
-  if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows)) return;
+  bool single;
+  if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows, &single)) return;
   const int n0 = cb * PBN;
   const uint32_t k0 = (uint32_t)seg * (uint32_t)klen * 2u;  // segment start, bytes
 
@@ -496,12 +521,21 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   float* ys = y + (size_t)seg * R * H + n0;
   if constexpr (C::MT > 1) {
     if (rows <= C::PBM / 2) {  // as in gate/up
-      gemm2_tile<C, C::MT / 2, DT>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots,
-                                   ys);
+      if (C::NT_WEIGHTS && single)
+        gemm2_tile<C, C::MT / 2, DT, C::NT_WEIGHTS>(sb, d, klen / C::PBK, rows, p0, H, gates_flat,
+                                           sorted_slots, ys);
+      else
+        gemm2_tile<C, C::MT / 2, DT, false>(sb, d, klen / C::PBK, rows, p0, H, gates_flat,
+                                            sorted_slots, ys);
       return;
     }
   }
-  gemm2_tile<C, C::MT, DT>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots, ys);
+  if (C::NT_WEIGHTS && single)
+    gemm2_tile<C, C::MT, DT, C::NT_WEIGHTS>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots,
+                                   ys);
+  else
+    gemm2_tile<C, C::MT, DT, false>(sb, d, klen / C::PBK, rows, p0, H, gates_flat, sorted_slots,
+                                    ys);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
