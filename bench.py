@@ -96,6 +96,7 @@ def kernel_breakdown(m, inp, reps: int) -> dict:
     n, hidden = x.shape
     e, inter, _ = w1.shape
     stream = _capi.stream_of(x.device)
+    tiled = m.uses_tiled_gemms(n, budget, e, inter)
     names = ["route", "gemm1", "gemm2", "combine"]
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(reps)]
     out = torch.empty_like(x)
@@ -104,22 +105,40 @@ def kernel_breakdown(m, inp, reps: int) -> dict:
         routing = m.route_experts(x, router, accept, budget, inter)
         ws = routing.ws
         ev[r][1].record()
-        _capi.call("tm_op1_gemm1", x.data_ptr(), w1.data_ptr(), w3.data_ptr(), ws.h.data_ptr(),
-                   routing.sorted_slots.data_ptr(), routing.tiles.data_ptr(),
-                   routing.max_tiles, n, hidden, inter, e, _capi.TM_DTYPE_BF16, stream)
-        ev[r][2].record()
-        _capi.call("tm_op1_gemm2", ws.h.data_ptr(), w2.data_ptr(), ws.partial.data_ptr(),
-                   routing.gates_flat.data_ptr(), routing.sorted_slots.data_ptr(),
-                   routing.tiles.data_ptr(), routing.max_tiles, ws.split, n, hidden, inter, e,
-                   _capi.TM_DTYPE_BF16, stream)
+        # the same launches as tree_moe_forward (op1_tree_moe.py): the tiled
+        # pair or the weight-streaming pair, then the combine
+        split = ws.split
+        if tiled:
+            split = m._tiled_split(n, budget, e, hidden, inter, ws)
+            _capi.call("tm_op1_prefill_gemm1", x.data_ptr(), w1.data_ptr(), w3.data_ptr(),
+                       ws.h.data_ptr(), routing.sorted_slots.data_ptr(),
+                       routing.expert_offsets.data_ptr(), routing.tiles.data_ptr(),
+                       routing.max_tiles, n, hidden, inter, e, _capi.TM_DTYPE_BF16, stream)
+            ev[r][2].record()
+            _capi.call("tm_op1_prefill_gemm2", ws.h.data_ptr(), w2.data_ptr(),
+                       ws.partial.data_ptr(), routing.gates_flat.data_ptr(),
+                       routing.sorted_slots.data_ptr(), routing.expert_offsets.data_ptr(),
+                       routing.tiles.data_ptr(), routing.max_tiles, split, n, hidden, inter, e,
+                       _capi.TM_DTYPE_BF16, stream)
+        else:
+            _capi.call("tm_op1_gemm1", x.data_ptr(), w1.data_ptr(), w3.data_ptr(),
+                       ws.h.data_ptr(), routing.sorted_slots.data_ptr(),
+                       routing.tiles.data_ptr(), routing.max_tiles, n, hidden, inter, e,
+                       _capi.TM_DTYPE_BF16, stream)
+            ev[r][2].record()
+            _capi.call("tm_op1_gemm2", ws.h.data_ptr(), w2.data_ptr(), ws.partial.data_ptr(),
+                       routing.gates_flat.data_ptr(), routing.sorted_slots.data_ptr(),
+                       routing.tiles.data_ptr(), routing.max_tiles, split, n, hidden, inter,
+                       e, _capi.TM_DTYPE_BF16, stream)
         ev[r][3].record()
         _capi.call("tm_op1_combine", ws.partial.data_ptr(), routing.slot_pos.data_ptr(),
-                   out.data_ptr(), n, hidden, ws.split, _capi.TM_DTYPE_BF16, stream)
+                   out.data_ptr(), n, hidden, split, _capi.TM_DTYPE_BF16, stream)
         ev[r][4].record()
     torch.cuda.synchronize()
     res = {}
     for k, name in enumerate(names):
         res[name] = median([ev[r][k].elapsed_time(ev[r][k + 1]) for r in range(reps)])
+    res["tiled"] = tiled
     return res
 
 
@@ -213,6 +232,8 @@ def main():
     for _ in range(10):
         fwd()
     bd = kernel_breakdown(m, inp, reps)
+    tiled = bd.pop("tiled")
+    gemm1_kernel = "tm_prefill_gemm1_kernel<Tile<128, 64, 3>>" if tiled else "tm_gemm1_kernel"
     # algorithmic bytes per launch: one read of the active experts' weights
     # (w1 + w3 for gemm1, w2 for gemm2) plus the activation rows in (x); the
     # h and fp32-partial workspaces are not counted
@@ -245,7 +266,7 @@ def main():
         "config": {"workload": "op1 Mixtral-8x7B MoE layer, T=64 tree tokens, top-2, B=8 (config 2)",
                    "tokens": t, "hidden": h, "ffn": i, "experts": e, "budget": inp.budget,
                    "active_experts": n_active, "bytes_alg": bytes_alg, "flops_alg": flops},
-        "roofline": {"bound": "hbm", "kernel": "tm_gemm1_kernel",
+        "roofline": {"bound": "hbm", "kernel": gemm1_kernel,
                      "achieved": round(gemm1_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gemm1_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "bytes_alg_per_launch": gemm1_bytes,

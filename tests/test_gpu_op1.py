@@ -323,6 +323,7 @@ def _force_path(monkeypatch, path):
     or the MFMA-tiled ones ("tiled") whatever the rows per expert."""
     m = _op1()
     monkeypatch.setattr(m, "TILED_MIN_ROWS", 1 << 30 if path == "stream" else 1)
+    monkeypatch.setattr(m, "TILED_MIN_ROWS_WIDE", 1 << 30 if path == "stream" else 1)
 
 
 @pytest.mark.parametrize("path", ["stream", "tiled"])
@@ -504,7 +505,8 @@ def test_tiled_and_streaming_gemms_agree(monkeypatch):
     again = m.tree_moe_forward(*dev, 8)
     assert torch.equal(tiled, again)
     monkeypatch.setattr(m, "TILED_MIN_ROWS", 1 << 30)
-    assert not m.uses_tiled_gemms(512, 8, 8)
+    monkeypatch.setattr(m, "TILED_MIN_ROWS_WIDE", 1 << 30)
+    assert not m.uses_tiled_gemms(512, 8, 8, 2048)
     streaming = m.tree_moe_forward(*dev, 8)
     assert op1_ref.rel_l2(tiled.float().cpu(), streaming.float().cpu()) <= 5e-3
 

@@ -327,3 +327,21 @@ def test_routing_token_count_mismatch_raises_before_launch(monkeypatch):
     with pytest.raises(ValueError, match="different shape"):
         m.tree_moe_forward(x, w1, w2, w1, torch.zeros(e, h, dtype=bf), torch.ones(65), 8,
                            routing=r)
+
+
+def test_gemm_path_rule():
+    """The MFMA-tiled GEMMs run from 32 rows per routed expert, and from 8
+    rows when the FFN is 7168 wide or more (the Mixtral decode shape T=64,
+    B=8, I=14336 takes them); narrow FFN shares keep the weight-streaming
+    GEMMs until 32 rows."""
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+
+    assert m.uses_tiled_gemms(64, 8, 8, 14336)        # config 2: 16 rows, wide
+    assert m.uses_tiled_gemms(32, 8, 8, 14336)        # 8 rows, wide
+    assert not m.uses_tiled_gemms(16, 8, 8, 14336)    # 4 rows
+    assert m.uses_tiled_gemms(64, 8, 8, 7168)         # the TP-2 share
+    assert not m.uses_tiled_gemms(64, 8, 8, 3584)     # TP-4 and narrower stream
+    assert not m.uses_tiled_gemms(64, 8, 8)           # no width given: 32-row rule
+    assert m.uses_tiled_gemms(64, 4, 8, 3584)         # config 3: 32 rows
+    assert m.uses_tiled_gemms(128, 8, 8, 1792)
+

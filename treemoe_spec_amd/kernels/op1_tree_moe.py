@@ -52,17 +52,27 @@ def compact_block_capacity(num_slots: int, expert_budget: int, block_m: int = BM
 
 
 # Rows per active expert from which the MFMA-tiled GEMMs (128-row tiles that
-# reuse each weight tile across rows) replace the weight-streaming GEMMs
-# (one pass over an expert's weights per 64-row tile).  Measured at the
-# Mixtral shape: 16 rows per expert (T=64, B=8) stream faster (501 vs 567 us),
-# from 32 (T=64, B=4 skewed; T=128, B=8) the tiled pair wins (306 vs 340 us,
-# 570 vs 598 us), and by 64 rows it takes 0.6x the streaming time.
-TILED_MIN_ROWS = 32
+# reuse each weight tile across rows) replace the weight-streaming GEMMs (one
+# pass over an expert's weights per 64-row tile).  The tiled pair streams a
+# single-tile expert's weights with the non-temporal policy, so it also wins
+# at few rows per expert when the FFN is wide enough to fill the chip with
+# column jobs.  Measured at the Mixtral shape (H=4096, E=8, B=8, forward us,
+# streaming / tiled): I=14336 at 8 rows per expert (T=32) 459 / 453, 16 rows
+# (T=64, config 2) 476 / 457, 32 rows (T=128) 609 / 477; at 4 rows (T=16)
+# 436 / 448; 16 rows with I=7168 263 / 243, I=3584 149 / 157, I=1792 91 / 107.
+TILED_MIN_ROWS = 32           # tiled from this many rows per routed expert ..
+TILED_MIN_ROWS_WIDE = 8       # .. or from this many when inter >= TILED_WIDE_INTER
+TILED_WIDE_INTER = 7168
 
 
-def uses_tiled_gemms(num_tokens: int, expert_budget: int, num_experts: int) -> bool:
-    """True when the average rows per routed expert reach TILED_MIN_ROWS."""
-    return 2 * num_tokens >= TILED_MIN_ROWS * min(expert_budget, num_experts)
+def uses_tiled_gemms(num_tokens: int, expert_budget: int, num_experts: int,
+                     inter: int = 0) -> bool:
+    """True when the average rows per routed expert reach TILED_MIN_ROWS, or
+    TILED_MIN_ROWS_WIDE for an intermediate size of TILED_WIDE_INTER or more."""
+    active = min(expert_budget, num_experts)
+    if 2 * num_tokens >= TILED_MIN_ROWS * active:
+        return True
+    return inter >= TILED_WIDE_INTER and 2 * num_tokens >= TILED_MIN_ROWS_WIDE * active
 
 
 def _split_for(inter: int) -> int:
@@ -401,7 +411,7 @@ def tree_moe_forward(
         raise ValueError("routing was computed for a different shape")
     stream = _capi.stream_of(x.device)
     split = ws.split
-    if uses_tiled_gemms(n, expert_budget, e):
+    if uses_tiled_gemms(n, expert_budget, e, inter):
         split = _tiled_split(n, expert_budget, e, hidden, inter, ws)
         call("tm_op1_prefill_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h),
              ptr(routing.sorted_slots), ptr(routing.expert_offsets), ptr(routing.tiles),
