@@ -155,6 +155,7 @@ def test_argument_errors_return_before_launch(call, expect):
     from treemoe_spec_amd import _capi
 
     name, *args = call
+    assert len(args) == len(_capi.SIGNATURES[name]), "argument count"
     fn = getattr(_capi.lib(), name)
     assert fn(*args) == expect
 
