@@ -269,9 +269,11 @@ def fused_verify_commit(
     csr, num_edges = _cached_csr(children, n, dev)
     # fresh outputs every call (the reference returns new tensors): one
     # allocation holding accepted_slots [N], accepted_tokens [N] and
-    # (bonus, num_accepted, next_root)
+    # (bonus, num_accepted, next_root); the launches take its addresses, and
+    # its views are made while the device runs them
     out = torch.empty(2 * n + 3, dtype=torch.int64, device=dev)
-    slots, toks, result = out.split((n, n, 3))
+    p_slots = out.data_ptr()
+    p_toks, p_result = p_slots + 8 * n, p_slots + 16 * n
     stream = _capi.stream_of(dev)
     c_start, c_count, c_list = ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n
     if temperature != 0.0:
@@ -285,8 +287,8 @@ def fused_verify_commit(
         residual = torch.empty(v, dtype=torch.float32, device=dev)
         call("tm_op4_sample_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
              ptr(q), q.stride(0), ptr(tokens), c_start, c_count, c_list, num_edges,
-             ptr(uniforms), ptr(bonus_u), float(temperature), ptr(residual), ptr(slots),
-             ptr(toks), ptr(result), stream)
+             ptr(uniforms), ptr(bonus_u), float(temperature), ptr(residual), p_slots, p_toks,
+             p_result, stream)
         commit_depth = _tree_depth(children)
     else:
         if rep_penalty != 1.0:
@@ -294,12 +296,13 @@ def fused_verify_commit(
         ws = _scratch(n, dev)
         args = (ptr(target_logits), dtype, n, v, target_logits.stride(0), ptr(tokens), c_start,
                 c_count, c_list, num_edges, max_depth, 1 if rep_penalty != 1.0 else 0,
-                ptr(ws.argmax), ptr(slots), ptr(toks), ptr(result), ptr(ws.partials), stream)
+                ptr(ws.argmax), p_slots, p_toks, p_result, ptr(ws.partials), stream)
         if _fast is not None:
             check(_fast.argmax_walk(*args), "tm_op4_argmax_walk")
         else:
             call("tm_op4_argmax_walk", *args)
         commit_depth = max_depth
+    slots, toks, result = out.split((n, n, 3))
     bonus, num, _ = result.unbind()
     res = VerifyResult(accepted_slots=slots, accepted_tokens=toks, bonus_token=bonus,
                        num_accepted=num)
