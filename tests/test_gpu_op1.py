@@ -511,6 +511,19 @@ def test_tiled_and_streaming_gemms_agree(monkeypatch):
     assert op1_ref.rel_l2(tiled.float().cpu(), streaming.float().cpu()) <= 5e-3
 
 
+@pytest.mark.parametrize("t,e,i,budget", [(256, 8, 1792, 8), (100, 16, 1280, 6), (64, 8, 1792, 4)])
+def test_tiled_gemms_ragged_column_blocks(t, e, i, budget, monkeypatch):
+    """Column blocks that do not divide evenly among the 8 XCDs (I / 128 = 14
+    or 10 blocks, so some launch indices map to no job) on the MFMA-tiled
+    GEMMs, with 8 and 16 experts: the layer meets the fp64 golden."""
+    _say(f"tiled ragged columns t={t} E={e} I={i} B={budget}")
+    _force_path(monkeypatch, "tiled")
+    out, golden, _, _ = _forward_and_golden(t, e, 512, i, budget, 71 + t)
+    err = op1_ref.rel_l2(out.cpu().float(), golden)
+    _say(f"  rel_l2={err:.3e}")
+    assert err <= REL_L2_TOL
+
+
 def test_tiled_down_gemm_segment_counts_agree(monkeypatch):
     """The tiled path at a small shape takes 4 K segments for the down GEMM;
     forced back to 2 it must give the same layer up to fp32 summation order,
