@@ -139,6 +139,7 @@ def kernel_breakdown(m, inp, reps: int) -> dict:
     for k, name in enumerate(names):
         res[name] = median([ev[r][k].elapsed_time(ev[r][k + 1]) for r in range(reps)])
     res["tiled"] = tiled
+    res["max_tiles"] = routing.max_tiles
     return res
 
 
@@ -233,7 +234,9 @@ def main():
         fwd()
     bd = kernel_breakdown(m, inp, reps)
     tiled = bd.pop("tiled")
-    gemm1_kernel = "tm_prefill_gemm1_kernel<Tile<128, 64, 3>>" if tiled else "tm_gemm1_kernel"
+    max_tiles = bd.pop("max_tiles")
+    gemm1_kernel = (f"tm_prefill_gemm1_kernel<{m.tiled_gate_up_tile(t, e, max_tiles)}>"
+                    if tiled else "tm_gemm1_kernel")
     # algorithmic bytes per launch: one read of the active experts' weights
     # (w1 + w3 for gemm1, w2 for gemm2) plus the activation rows in (x); the
     # h and fp32-partial workspaces are not counted

@@ -171,8 +171,9 @@ int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out,
 
 /*
  * Gate/up projection + SwiGLU for many rows per expert (prefill / batched
- * trees), MFMA-tiled over 128 sorted rows (256 when 2T >= 384 E) x (128 w1 +
- * the same 128 w3) weight rows.  Same maths as
+ * trees), MFMA-tiled over 128 sorted rows x (128 w1 + the same 128 w3) weight
+ * rows; 256 rows when 2T >= 384 E, and 64 rows x (64 + 64) weight rows when
+ * 2T <= 16 max_tiles (few rows per active expert).  Same maths as
  * tm_op1_gemm1 and the reference `_moe_gemm1_kernel`
  * (treemoe/kernels/op1_tree_moe.py:300-383), but h is written ROW-MAJOR:
  *   h[p, n] = bf16( silu(x[sorted_slots[p] / 2] . w1[e, n]) * (... . w3[e, n]) )

@@ -345,3 +345,19 @@ def test_gemm_path_rule():
     assert m.uses_tiled_gemms(64, 4, 8, 3584)         # config 3: 32 rows
     assert m.uses_tiled_gemms(128, 8, 8, 1792)
 
+
+
+def test_tiled_gate_up_tile_rule():
+    """The gate/up tile the library picks (named in bench lines): 256-row tiles
+    from 384 rows per expert, the 64-row decode tile when the tile list
+    leaves at most 16 rows per entry, else 128-row tiles."""
+    from treemoe_spec_amd.kernels import op1_tree_moe as m
+
+    def tiles(t, budget, e=8):
+        return m.compact_block_limit(2 * t, budget, m.TILE_M)
+
+    assert m.tiled_gate_up_tile(64, 8, tiles(64, 8)) == "Tile<64, 64, 3, 128, 256>"   # config 2
+    assert m.tiled_gate_up_tile(64, 8, tiles(64, 4)) == "Tile<128, 64, 3>"            # config 3
+    assert m.tiled_gate_up_tile(2048, 8, tiles(2048, 8)) == "Tile<256, 32, 4>"        # config 5
+    assert m.tiled_gate_up_tile(32, 8, tiles(32, 8)) == "Tile<64, 64, 3, 128, 256>"
+    assert m.tiled_gate_up_tile(128, 8, tiles(128, 8)) == "Tile<128, 64, 3>"

@@ -38,17 +38,20 @@
 
 namespace {
 
-constexpr int PBN = 256;                 // weight rows per workgroup
-constexpr int NT = 512;                  // threads per workgroup (8 waves)
-constexpr int HSTRIDE = 128 * 2 + 16;    // bf16 h staging row stride (128 columns), bytes
+constexpr int HSTRIDE = 128 * 2 + 16;    // bf16 h staging row stride (up to 128 columns), bytes
 constexpr uint32_t kOOR = 0x80000000u;   // out-of-range buffer offset: loads 0
 
-// Tile configuration: BM sorted rows per M-tile, K steps of BK, NS stages.
-template <int BM, int BK, int NS>
+// Tile configuration: BM sorted rows per M-tile, K steps of BK, NS stages,
+// BN weight rows per workgroup, NTH threads (NTH / 64 waves as 2 row halves x
+// NTH / 128 column groups of 32 outputs, so BN = 32 x waves).
+template <int BM, int BK, int NS, int BN = 256, int NTH = 512>
 struct Tile {
   static constexpr int PBM = BM;
   static constexpr int PBK = BK;
   static constexpr int NSTAGE = NS;
+  static constexpr int PBN = BN;                  // weight rows per workgroup
+  static constexpr int NT = NTH;                  // threads per workgroup
+  static constexpr int NW = NTH / 64;             // waves
   static constexpr int PROW = PBK * 2;            // LDS row, bytes (PROW / 16 swizzled chunks)
   static constexpr int CPR = PROW / 16;           // 16-byte chunks per row
   static constexpr int RPB = 256 / PROW;          // rows per 256 B (one pass over the 64 banks)
@@ -67,12 +70,17 @@ struct Tile {
   // h rows staged per stage: the whole tile in one stage when it fits
   static constexpr int HROWS = PBM * HSTRIDE <= STAGE ? PBM : PBM / NSTAGE;
   static_assert(ALD >= 1 && BLD >= 1 && BLD % 2 == 0 && CPR >= 4, "tile shape");
+  static_assert(PBN == 32 * NW && (NW == 4 || NW == 8), "wave layout");
   static_assert(NS == 3 || NS == 4, "stage rotation");
   static_assert(HROWS * HSTRIDE <= STAGE && (PBM + HROWS - 1) / HROWS <= NS, "h staging");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
 };
 using Tile128 = Tile<128, 64, 3>;
 using Tile256 = Tile<256, 32, 4>;
+// Few rows per expert: 64-row M-tiles against 128 weight rows with 4 waves,
+// 72 KB of LDS, so two workgroups share a CU.  Same per-output K order as
+// Tile128, so the same bits.
+using TileDec = Tile<64, 64, 3, 128, 256>;
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -210,7 +218,7 @@ struct DmaLoad {
 // Row of load i for this thread, and the logical chunk it fetches.
 template <class C>
 __device__ __forceinline__ int dma_row(int i) {
-  return C::RPK * (8 * i + (threadIdx.x >> 6)) + ((threadIdx.x & 63) / C::CPR);
+  return C::RPK * (C::NW * i + (threadIdx.x >> 6)) + ((threadIdx.x & 63) / C::CPR);
 }
 template <class C>
 __device__ __forceinline__ int dma_chunk(int row) {
@@ -242,15 +250,15 @@ __device__ __forceinline__ void dma_step(const DmaLoad<C>& d, uint8_t* st, int k
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));  // LDS base: wave-uniform
 #pragma unroll
   for (int i = 0; i < C::ALD; ++i)
-    lds_load16(d.ra, st + (8 * i + w) * 1024,
+    lds_load16(d.ra, st + (C::NW * i + w) * 1024,
                (valid && d.aoff[i] != kOOR) ? d.aoff[i] + kb : kOOR);
 #pragma unroll
   for (int i = 0; i < C::BLD; ++i)
     if constexpr (NTB)
-      lds_load16_nt(i < C::BLD / 2 ? d.rb0 : d.rb1, st + C::ABYTES + (8 * i + w) * 1024,
+      lds_load16_nt(i < C::BLD / 2 ? d.rb0 : d.rb1, st + C::ABYTES + (C::NW * i + w) * 1024,
                     valid ? d.boff[i] + kb : kOOR);
     else
-      lds_load16(i < C::BLD / 2 ? d.rb0 : d.rb1, st + C::ABYTES + (8 * i + w) * 1024,
+      lds_load16(i < C::BLD / 2 ? d.rb0 : d.rb1, st + C::ABYTES + (C::NW * i + w) * 1024,
                  valid ? d.boff[i] + kb : kOOR);
 }
 
@@ -357,7 +365,7 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
   // accumulator column blocks: j = 0 -> w1 rows 32 wn ..; j = 1 -> the same w3 rows
-  const int brow[2] = {32 * wn, PBN / 2 + 32 * wn};
+  const int brow[2] = {32 * wn, C::PBN / 2 + 32 * wn};
   k_loop<C, M, DT, NTB>(sb, d, nk, brow, acc);
 #pragma unroll
   for (int i = 0; i < M; ++i)
@@ -371,10 +379,11 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
       *reinterpret_cast<uint16_t*>(h_stage<C>(sb, m) + c * 2) = Half16<DT>::round(hv);
     }
   __syncthreads();
+  constexpr int PPR = C::PBN / 16;  // 16-byte pieces of an h row (PBN / 2 columns)
 #pragma unroll
-  for (int j = 0; j < 64 * M * 16 / NT; ++j) {
-    const int piece = tid + NT * j;  // 64 M rows x 16 pieces of 16 B
-    const int r = piece >> 4, c16 = piece & 15;
+  for (int j = 0; j < 64 * M * PPR / C::NT; ++j) {
+    const int piece = tid + C::NT * j;  // 64 M rows x PPR pieces
+    const int r = piece / PPR, c16 = piece % PPR;
     if (r < rows) {
       const u32x4_t v = *reinterpret_cast<const u32x4_t*>(h_stage<C>(sb, r) + c16 * 16);
       *reinterpret_cast<u32x4_t*>(h + (size_t)(p0 + r) * I + n0 + c16 * 8) = v;
@@ -383,7 +392,7 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
 }
 
 template <class C, int DT>
-__global__ void __launch_bounds__(NT)
+__global__ void __launch_bounds__(C::NT)
 tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
                         const uint16_t* __restrict__ w3, uint16_t* __restrict__ h,
                         const int32_t* __restrict__ sorted_slots,
@@ -395,13 +404,13 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   __shared__ __attribute__((aligned(16))) uint8_t s3[C::NSTAGE > 3 ? C::STAGE : 16];
   const Stages sb{s0, s1, s2, s3};
   int mt, cb;
-  const int ncol = I / (PBN / 2);
+  const int ncol = I / (C::PBN / 2);
   const int n_mt = min(count_mtiles<C>(offsets, E), mt_max);
   if (!job_of((int)blockIdx.x, n_mt, ncol, &mt, &cb)) return;
   int e, p0, rows;
   bool single;
   if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows, &single)) return;
-  const int n0 = cb * (PBN / 2);  // first h column of the block
+  const int n0 = cb * (C::PBN / 2);  // first h column of the block
 
   DmaLoad<C> d;
   d.ra = pbuf(x, x_bytes);
@@ -418,7 +427,7 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
 #pragma unroll
   for (int i = 0; i < C::BLD; ++i) {
     const int r = dma_row<C>(i);  // first half of the loads: w1 rows; second: the same w3 rows
-    d.boff[i] = (uint32_t)(n0 + (r & (PBN / 2 - 1))) * (uint32_t)H * 2u +
+    d.boff[i] = (uint32_t)(n0 + (r & (C::PBN / 2 - 1))) * (uint32_t)H * 2u +
                 (uint32_t)dma_chunk<C>(r) * 16u;
   }
   // a tile with at most BM / 2 real rows (an expert's last) runs half the
@@ -479,7 +488,7 @@ __device__ __forceinline__ void gemm2_tile(const Stages& sb, const DmaLoad<C>& d
 }
 
 template <class C, int DT>
-__global__ void __launch_bounds__(NT)
+__global__ void __launch_bounds__(C::NT)
 tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restrict__ w2,
                         float* __restrict__ y, const float* __restrict__ gates_flat,
                         const int32_t* __restrict__ sorted_slots,
@@ -490,8 +499,9 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   __shared__ __attribute__((aligned(16))) uint8_t s1[C::STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t s2[C::STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t s3[C::NSTAGE > 3 ? C::STAGE : 16];
+  static_assert(C::NW == 8, "down GEMM: 8 waves, 64 output columns per column group");
   int mt, job;  // job = (column block, segment)
-  const int ncol = (H / PBN) * nsplit;
+  const int ncol = (H / C::PBN) * nsplit;
   const int n_mt = min(count_mtiles<C>(offsets, E), mt_max);
   if (!job_of((int)blockIdx.x, n_mt, ncol, &mt, &job)) return;
   const int cb = job / nsplit;
@@ -499,7 +509,7 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   int e, p0, rows;
   bool single;
   if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows, &single)) return;
-  const int n0 = cb * PBN;
+  const int n0 = cb * C::PBN;
   const uint32_t k0 = (uint32_t)seg * (uint32_t)klen * 2u;  // segment start, bytes
 
   DmaLoad<C> d;
@@ -540,15 +550,21 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
 
 bool aligned16(const void* p) { return ((uintptr_t)p % 16) == 0; }
 
+// The gate/up launch with tile C: jobs for the M-tile bound (the tile list's
+// length, capped by what 2T rows in E experts can take).
 template <class C, int DT>
-void launch_gemm1(const void* x, const void* w1, const void* w3, void* h,
-                  const int32_t* sorted_slots, const int32_t* expert_offsets,
-                  const int32_t* tiles, int64_t max_tiles, int64_t T, int64_t H, int64_t I,
-                  int64_t E, int64_t mt_max, int64_t jobs, hipStream_t stream) {
-  hipLaunchKernelGGL((tm_prefill_gemm1_kernel<C, DT>), dim3((unsigned)jobs), dim3(NT), 0, stream,
+int launch_gemm1(const void* x, const void* w1, const void* w3, void* h,
+                 const int32_t* sorted_slots, const int32_t* expert_offsets,
+                 const int32_t* tiles, int64_t max_tiles, int64_t T, int64_t H, int64_t I,
+                 int64_t E, hipStream_t stream) {
+  const int64_t mt_max = std::min<int64_t>(max_tiles, mtile_bound<C>(2 * T, E));
+  const int64_t jobs = launch_jobs(mt_max, I / (C::PBN / 2));
+  if (jobs > INT32_MAX) return TM_ERR_SHAPE;
+  hipLaunchKernelGGL((tm_prefill_gemm1_kernel<C, DT>), dim3((unsigned)jobs), dim3(C::NT), 0, stream,
                      (const uint16_t*)x, (const uint16_t*)w1, (const uint16_t*)w3,
                      (uint16_t*)h, sorted_slots, expert_offsets, tiles, (int)max_tiles,
                      (int)E, (int)H, (int)I, (int)mt_max, (uint32_t)(T * H * 2));
+  return TM_OK;
 }
 
 }  // namespace
@@ -560,33 +576,41 @@ extern "C" int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w
   if (T < 1 || T > TM_MAX_TOKENS || E < 2 || E > TM_MAX_EXPERTS || max_tiles < 1)
     return TM_ERR_SHAPE;
   if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
-  if (H < Tile128::PBK || (H % Tile128::PBK) != 0 || I < PBN / 2 || (I % (PBN / 2)) != 0)
+  if (H < Tile128::PBK || (H % Tile128::PBK) != 0 || I < Tile128::PBN / 2 ||
+      (I % (Tile128::PBN / 2)) != 0)
     return TM_ERR_SHAPE;
   if (I * H * 2 >= (int64_t)kOOR || T * H * 2 >= (int64_t)kOOR || 2 * T * I * 2 >= (int64_t)kOOR)
     return TM_ERR_SHAPE;
   if (!aligned16(x) || !aligned16(w1) || !aligned16(w3) || !aligned16(h)) return TM_ERR_ALIGN;
   // 256-row tiles when the experts average 384 rows or more: they read fewer
   // operand bytes per flop, but below that their coarser jobs and padding
-  // cost more than that saves (measured at the Mixtral shape)
+  // cost more than that saves (measured at the Mixtral shape).  TileDec when
+  // the tile list leaves at most 16 rows per entry (2T <= 16 max_tiles: few
+  // rows per active expert, e.g. 64 tree tokens over 8 experts): half the
+  // weight rows per workgroup and two workgroups per CU stream the weights
+  // faster there (config 2 gate/up 302 -> 289 us same-box).
   const bool big = 2 * T >= 384 * E;
-  const int64_t mt_max = std::min<int64_t>(
-      max_tiles, big ? mtile_bound<Tile256>(2 * T, E) : mtile_bound<Tile128>(2 * T, E));
-  const int64_t jobs = launch_jobs(mt_max, I / (PBN / 2));
-  if (jobs > INT32_MAX) return TM_ERR_SHAPE;
+  const bool dec = !big && 2 * T <= 16 * max_tiles;
   const hipStream_t st = (hipStream_t)stream;
-  if (big && dtype == TM_DTYPE_F16) {
-    launch_gemm1<Tile256, TM_DTYPE_F16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
-                                        max_tiles, T, H, I, E, mt_max, jobs, st);
-  } else if (big) {
-    launch_gemm1<Tile256, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
-                                         max_tiles, T, H, I, E, mt_max, jobs, st);
-  } else if (dtype == TM_DTYPE_F16) {
-    launch_gemm1<Tile128, TM_DTYPE_F16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
-                                        max_tiles, T, H, I, E, mt_max, jobs, st);
+  const bool f16 = dtype == TM_DTYPE_F16;
+  int rc;
+  if (big) {
+    rc = f16 ? launch_gemm1<Tile256, TM_DTYPE_F16>(x, w1, w3, h, sorted_slots, expert_offsets,
+                                                   tiles, max_tiles, T, H, I, E, st)
+             : launch_gemm1<Tile256, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets,
+                                                    tiles, max_tiles, T, H, I, E, st);
+  } else if (dec) {
+    rc = f16 ? launch_gemm1<TileDec, TM_DTYPE_F16>(x, w1, w3, h, sorted_slots, expert_offsets,
+                                                   tiles, max_tiles, T, H, I, E, st)
+             : launch_gemm1<TileDec, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets,
+                                                    tiles, max_tiles, T, H, I, E, st);
   } else {
-    launch_gemm1<Tile128, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets, tiles,
-                                         max_tiles, T, H, I, E, mt_max, jobs, st);
+    rc = f16 ? launch_gemm1<Tile128, TM_DTYPE_F16>(x, w1, w3, h, sorted_slots, expert_offsets,
+                                                   tiles, max_tiles, T, H, I, E, st)
+             : launch_gemm1<Tile128, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets,
+                                                    tiles, max_tiles, T, H, I, E, st);
   }
+  if (rc) return rc;
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
@@ -602,15 +626,15 @@ extern "C" int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y,
   if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (split < 1 || (I % split) != 0) return TM_ERR_SHAPE;
   const int64_t klen = I / split;
-  if (klen < C::PBK || (klen % C::PBK) != 0 || H < PBN || (H % PBN) != 0) return TM_ERR_SHAPE;
+  if (klen < C::PBK || (klen % C::PBK) != 0 || H < C::PBN || (H % C::PBN) != 0) return TM_ERR_SHAPE;
   if (H * I * 2 >= (int64_t)kOOR || 2 * T * I * 2 >= (int64_t)kOOR) return TM_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w2) || !aligned16(y)) return TM_ERR_ALIGN;
   const int64_t mt_max = std::min<int64_t>(max_tiles, mtile_bound<C>(2 * T, E));
-  const int64_t jobs = launch_jobs(mt_max, (H / PBN) * split);
+  const int64_t jobs = launch_jobs(mt_max, (H / C::PBN) * split);
   if (jobs > INT32_MAX) return TM_ERR_SHAPE;
   hipLaunchKernelGGL((dtype == TM_DTYPE_F16 ? tm_prefill_gemm2_kernel<C, TM_DTYPE_F16>
                                             : tm_prefill_gemm2_kernel<C, TM_DTYPE_BF16>),
-                     dim3((unsigned)jobs), dim3(NT), 0,
+                     dim3((unsigned)jobs), dim3(C::NT), 0,
                      (hipStream_t)stream, (const uint16_t*)h, (const uint16_t*)w2, y, gates_flat,
                      sorted_slots, expert_offsets, tiles, (int)max_tiles, (int)E, (int)(2 * T),
                      (int)H, (int)I, (int)klen, (int)split, (int)mt_max,

@@ -75,6 +75,18 @@ def uses_tiled_gemms(num_tokens: int, expert_budget: int, num_experts: int,
     return inter >= TILED_WIDE_INTER and 2 * num_tokens >= TILED_MIN_ROWS_WIDE * active
 
 
+def tiled_gate_up_tile(num_tokens: int, num_experts: int, max_tiles: int) -> str:
+    """The tile tm_op1_prefill_gemm1 picks (the rule in op1_prefill.hip):
+    256-row tiles when the experts average 384 rows or more, the 64-row
+    decode tile when the tile list leaves at most 16 rows per entry, else
+    128-row tiles.  For naming kernels in measurements."""
+    if 2 * num_tokens >= 384 * num_experts:
+        return "Tile<256, 32, 4>"
+    if 2 * num_tokens <= 16 * max_tiles:
+        return "Tile<64, 64, 3, 128, 256>"
+    return "Tile<128, 64, 3>"
+
+
 def _split_for(inter: int) -> int:
     for s in (SPLIT_K, 2, 1):
         if s >= 1 and inter % s == 0 and (inter // s) % 256 == 0:
