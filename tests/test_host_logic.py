@@ -331,16 +331,17 @@ def test_routing_token_count_mismatch_raises_before_launch(monkeypatch):
 
 def test_gemm_path_rule():
     """The MFMA-tiled GEMMs run from 32 rows per routed expert, and from 8
-    rows when the FFN is 7168 wide or more (the Mixtral decode shape T=64,
-    B=8, I=14336 takes them); narrow FFN shares keep the weight-streaming
-    GEMMs until 32 rows."""
+    rows when the FFN is 3584 wide or more (the Mixtral decode shape T=64,
+    B=8, I=14336 and its TP-2 and TP-4 shares take them); narrower FFN
+    shares keep the weight-streaming GEMMs until 32 rows."""
     from treemoe_spec_amd.kernels import op1_tree_moe as m
 
     assert m.uses_tiled_gemms(64, 8, 8, 14336)        # config 2: 16 rows, wide
     assert m.uses_tiled_gemms(32, 8, 8, 14336)        # 8 rows, wide
     assert not m.uses_tiled_gemms(16, 8, 8, 14336)    # 4 rows
     assert m.uses_tiled_gemms(64, 8, 8, 7168)         # the TP-2 share
-    assert not m.uses_tiled_gemms(64, 8, 8, 3584)     # TP-4 and narrower stream
+    assert m.uses_tiled_gemms(64, 8, 8, 3584)         # the TP-4 share
+    assert not m.uses_tiled_gemms(64, 8, 8, 1792)     # TP-8 streams
     assert not m.uses_tiled_gemms(64, 8, 8)           # no width given: 32-row rule
     assert m.uses_tiled_gemms(64, 4, 8, 3584)         # config 3: 32 rows
     assert m.uses_tiled_gemms(128, 8, 8, 1792)

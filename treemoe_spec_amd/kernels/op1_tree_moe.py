@@ -51,18 +51,20 @@ def compact_block_capacity(num_slots: int, expert_budget: int, block_m: int = BM
     return 1 << max(logical - 1, 0).bit_length()
 
 
-# Rows per active expert from which the MFMA-tiled GEMMs (128-row tiles that
-# reuse each weight tile across rows) replace the weight-streaming GEMMs (one
-# pass over an expert's weights per 64-row tile).  The tiled pair streams a
+# Rows per active expert from which the MFMA-tiled GEMMs (tiles that reuse
+# each weight tile across rows) replace the weight-streaming GEMMs (one pass
+# over an expert's weights per 64-row tile).  The tiled pair streams a
 # single-tile expert's weights with the non-temporal policy, so it also wins
 # at few rows per expert when the FFN is wide enough to fill the chip with
 # column jobs.  Measured at the Mixtral shape (H=4096, E=8, B=8, forward us,
 # streaming / tiled): I=14336 at 8 rows per expert (T=32) 459 / 453, 16 rows
 # (T=64, config 2) 476 / 457, 32 rows (T=128) 609 / 477; at 4 rows (T=16)
-# 436 / 448; 16 rows with I=7168 263 / 243, I=3584 149 / 157, I=1792 91 / 107.
+# 436 / 448.  With the 64-row gate/up tile for few rows per expert, 16 rows
+# per expert: I=7168 262 / 242, I=3584 148 / 132 (8 rows 135 / 129; B=4 104 /
+# 100), I=1792 89 / 101 (8 rows 83 / 95).
 TILED_MIN_ROWS = 32           # tiled from this many rows per routed expert ..
 TILED_MIN_ROWS_WIDE = 8       # .. or from this many when inter >= TILED_WIDE_INTER
-TILED_WIDE_INTER = 7168
+TILED_WIDE_INTER = 3584
 
 
 def uses_tiled_gemms(num_tokens: int, expert_budget: int, num_experts: int,
