@@ -38,7 +38,6 @@
 
 namespace {
 
-constexpr int HSTRIDE = 128 * 2 + 16;    // bf16 h staging row stride (up to 128 columns), bytes
 constexpr uint32_t kOOR = 0x80000000u;   // out-of-range buffer offset: loads 0
 
 // Tile configuration: BM sorted rows per M-tile, K steps of BK, NS stages,
@@ -67,7 +66,9 @@ struct Tile {
   // for tiles of at most 128 rows; the 256-row gate/up tile runs where most
   // experts take several M-tiles, and there the policy measured slower
   static constexpr bool NT_WEIGHTS = BM <= 128;
-  // h rows staged per stage: the whole tile in one stage when it fits
+  // bf16 h staging: rows of PBN / 2 columns, padded by 16 bytes; rows per
+  // stage: the whole tile in one stage when it fits
+  static constexpr int HSTRIDE = PBN + 16;
   static constexpr int HROWS = PBM * HSTRIDE <= STAGE ? PBM : PBM / NSTAGE;
   static_assert(ALD >= 1 && BLD >= 1 && BLD % 2 == 0 && CPR >= 4, "tile shape");
   static_assert(PBN == 32 * NW && (NW == 4 || NW == 8), "wave layout");
@@ -344,7 +345,7 @@ template <class C>
 __device__ __forceinline__ uint8_t* h_stage(const Stages& sb, int m) {
   const int s = m / C::HROWS;
   uint8_t* base = s == 0 ? sb.s0 : s == 1 ? sb.s1 : s == 2 ? sb.s2 : sb.s3;
-  return base + (m % C::HROWS) * HSTRIDE;
+  return base + (m % C::HROWS) * C::HSTRIDE;
 }
 
 // The MFMAs and the epilogue of one gate/up tile with M accumulator tiles
