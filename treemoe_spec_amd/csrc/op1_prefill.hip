@@ -280,7 +280,7 @@ __device__ __forceinline__ u32x4_t frag(const uint8_t* tile, int row, int s, int
 
 // acc[i][j] += A[32 M wm + 32 i, :] B[brow[j], :]^T over one staged step.  M
 // (<= MT) is the accumulator tiles per wave along the rows: M = MT covers the
-// whole M-tile, M = MT / 2 its first half (a tile with at most BM / 2 real
+// whole M-tile, a smaller M its first 64 M rows (a tile with at most 64 M real
 // rows, whose other rows are zeros).
 template <class C, int M, int DT>
 __device__ __forceinline__ void compute_step(const uint8_t* st, const int (&brow)[2],
@@ -392,6 +392,22 @@ __device__ __forceinline__ void gemm1_tile(const Stages& sb, const DmaLoad<C>& d
   }
 }
 
+// gemm1_tile with the fewest accumulator tiles M <= MM per wave whose 64 M
+// rows (two waves of 32 M) cover `rows`.  Each output keeps the same K order
+// whatever M is, so the bits do not depend on it.
+template <class C, int MM, int DT, bool NTB>
+__device__ __forceinline__ void gemm1_rows(const Stages& sb, const DmaLoad<C>& d, int nk,
+                                           int rows, int p0, int n0, int I,
+                                           uint16_t* __restrict__ h) {
+  if constexpr (MM > 1) {
+    if (rows <= 64 * (MM - 1)) {
+      gemm1_rows<C, MM - 1, DT, NTB>(sb, d, nk, rows, p0, n0, I, h);
+      return;
+    }
+  }
+  gemm1_tile<C, MM, DT, NTB>(sb, d, nk, rows, p0, n0, I, h);
+}
+
 template <class C, int DT>
 __global__ void __launch_bounds__(C::NT)
 tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
@@ -431,23 +447,16 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
     d.boff[i] = (uint32_t)(n0 + (r & (C::PBN / 2 - 1))) * (uint32_t)H * 2u +
                 (uint32_t)dma_chunk<C>(r) * 16u;
   }
-  // a tile with at most BM / 2 real rows (an expert's last) runs half the
-  // MFMAs; its A rows past `rows` are loaded as zeros without memory traffic
-  // An expert that takes one M-tile has its weights read by this job alone:
-  // they stream through with the non-temporal policy (a load-only probe
-  // streams 7.1 TB/s with it, 6.2 without).  With several M-tiles the other
-  // jobs of the expert find them in L2, so those loads stay cached.
-  if constexpr (C::MT > 1) {
-    if (rows <= C::PBM / 2) {
-      if (C::NT_WEIGHTS && single)
-        gemm1_tile<C, C::MT / 2, DT, C::NT_WEIGHTS>(sb, d, H / C::PBK, rows, p0, n0, I, h);
-      else gemm1_tile<C, C::MT / 2, DT, false>(sb, d, H / C::PBK, rows, p0, n0, I, h);
-      return;
-    }
-  }
+  // A tile with fewer than BM real rows (an expert's last) runs the MFMAs of
+  // its first ceil(rows / 64) 64-row quarters only; its A rows past `rows`
+  // are loaded as zeros without memory traffic.  An expert that takes one
+  // M-tile has its weights read by this job alone: they stream through with
+  // the non-temporal policy (a load-only probe streams 7.1 TB/s with it, 6.2
+  // without).  With several M-tiles the other jobs of the expert find them in
+  // L2, so those loads stay cached.
   if (C::NT_WEIGHTS && single)
-    gemm1_tile<C, C::MT, DT, C::NT_WEIGHTS>(sb, d, H / C::PBK, rows, p0, n0, I, h);
-  else gemm1_tile<C, C::MT, DT, false>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+    gemm1_rows<C, C::MT, DT, C::NT_WEIGHTS>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+  else gemm1_rows<C, C::MT, DT, false>(sb, d, H / C::PBK, rows, p0, n0, I, h);
 }
 
 // ---------------------------------------------------------------- down --
