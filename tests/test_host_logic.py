@@ -281,9 +281,10 @@ def test_op4_commit_host_logic_with_reference_cache(monkeypatch):
     monkeypatch.setattr(op4_commit, "_fast", None)
     slots = torch.tensor([3, 9, 30] + [-1] * 61)
     result = torch.tensor([7, 3, 30])
-    op4_commit._commit(kv, slots, result, 64, 6, torch.device("cpu"), 0)
+    op4_commit._commit(kv, slots.data_ptr(), result.data_ptr(), 64, 6, torch.device("cpu"), 0)
     assert seen["name"] == "tm_op4_kv_commit"
     a = seen["args"]
+    assert a[9] == slots.data_ptr() and a[10] == result.data_ptr()
     assert a[8] == 64 and a[12] == 1 and a[14] == len(kv.block_table) and a[15] == 100
     assert a[16] == 6 and len(kv.block_table) * 64 >= 100 + 7
     table, scratch = op4_commit.device_tables_of(kv, "cpu")
@@ -299,7 +300,7 @@ def test_op4_commit_host_logic_with_reference_cache(monkeypatch):
     table2, _ = op4_commit.device_tables_of(kv, "cpu")
     assert table2.tolist() == kv.block_table
     with pytest.raises(ValueError, match="scratch"):
-        op4_commit._commit(kv, slots, result, 65, 6, torch.device("cpu"), 0)
+        op4_commit._commit(kv, slots.data_ptr(), result.data_ptr(), 65, 6, torch.device("cpu"), 0)
 
 
 def test_routing_token_count_mismatch_raises_before_launch(monkeypatch):

@@ -195,10 +195,12 @@ def _cached_csr(children: list[list[int]], n: int, device) -> tuple[torch.Tensor
     return csr, num_edges
 
 
-def _commit(kv, res_slots: torch.Tensor, result: torch.Tensor, n: int, commit_depth: int,
-            dev, stream: int, host_count: int = 0) -> None:
+def _commit(kv, p_slots: int, p_result: int, n: int, commit_depth: int, dev, stream: int,
+            host_count: int = 0) -> None:
     """Copy the KV rows of [root] + accepted path from the tree scratch to
-    positions seq_len, seq_len + 1, ... on the device; advance seq_len."""
+    positions seq_len, seq_len + 1, ... on the device (accepted slots and
+    result at device addresses p_slots, p_result); the caller advances
+    seq_len."""
     tree_pages = scratch_pages_of(kv)
     k, v = kv.k, kv.v
     if not (k.is_contiguous() and v.is_contiguous() and v.shape == k.shape and k.dim() == 5):
@@ -208,7 +210,7 @@ def _commit(kv, res_slots: torch.Tensor, result: torch.Tensor, n: int, commit_de
     kv._ensure_capacity(kv.seq_len + commit_depth + 1)   # reference :251
     table, scratch = device_tables_of(kv, dev)
     args = (ptr(k), ptr(v), k.element_size(), k.shape[0], k.shape[3] * k.shape[4], k.stride(0),
-            k.stride(1), k.stride(2), kv.block_size, ptr(res_slots), ptr(result), ptr(scratch),
+            k.stride(1), k.stride(2), kv.block_size, p_slots, p_result, ptr(scratch),
             len(tree_pages), ptr(table), len(kv.block_table), kv.seq_len, commit_depth,
             host_count, stream)
     if _fast is not None:
@@ -302,19 +304,21 @@ def fused_verify_commit(
         else:
             call("tm_op4_argmax_walk", *args)
         commit_depth = max_depth
+    if kv is not None:
+        # commit [root] + accepted path: the root token's KV (tree slot 0) is
+        # part of the committed sequence too (reference :242-247), launched
+        # right behind the walk.  The count comes back through the pinned
+        # word the commit writes (reference :267 reads it with a
+        # device-to-host copy).
+        ws = _scratch(n, dev)
+        note = ws.host_count()
+        if note:
+            ws.note_np[0] = -1
+        _commit(kv, p_slots, p_result, n, commit_depth, dev, stream, note)
     slots, toks, result = out.split((n, n, 3))
     bonus, num, _ = result.unbind()
     res = VerifyResult(accepted_slots=slots, accepted_tokens=toks, bonus_token=bonus,
                        num_accepted=num)
     if kv is not None:
-        # commit [root] + accepted path: the root token's KV (tree slot 0) is
-        # part of the committed sequence too (reference :242-247).  The count
-        # comes back through the pinned word the commit writes (reference
-        # :267 reads it with a device-to-host copy).
-        ws = _scratch(n, dev)
-        note = ws.host_count()
-        if note:
-            ws.note_np[0] = -1
-        _commit(kv, slots, result, n, commit_depth, dev, stream, note)
         kv.seq_len += _read_count(ws, result) + 1
     return res
