@@ -4,9 +4,10 @@
 // kernels (which re-read an expert's weights once per 64-row tile) are the
 // wrong shape.  These kernels tile both operands:
 //
-//   workgroup = 8 waves (2 x 4) = BM sorted rows x 256 weight rows; each wave
-//   owns BM/2 x 64 outputs = (BM/64) x 2 v_mfma_f32_32x32x16_bf16 tiles (on
-//   gfx950 the 32x32 form sustains ~2.2 PFLOP/s, the 16x16x32 form ~1.3).
+//   workgroup = NW waves (2 row halves x NW / 2 column groups) = BM sorted rows
+//   x 32 NW weight rows; each wave owns BM/2 x 64 outputs = (BM/64) x 2
+//   v_mfma_f32_32x32x16_bf16 tiles (on gfx950 the 32x32 form sustains ~2.2
+//   PFLOP/s, the 16x16x32 form ~1.3).
 //   Operands go from global memory straight into LDS (16-byte buffer loads
 //   with the LDS flag: lane i of a load lands at byte 16 i of its 1 KB block,
 //   no registers involved), NS stages deep: while the MFMAs of step k run,
@@ -15,14 +16,20 @@
 //   choosing each lane's source chunk; 16 consecutive rows read at one
 //   logical chunk then hit 16 distinct 4-bank groups.
 //
-// Two tile configurations: BM = 128 with K steps of 64 and three 48 KB
-// stages, and BM = 256 with K steps of 32 and four 32 KB stages (fewer
-// operand bytes per flop, larger jobs).  Down always uses the first; gate/up
-// uses the second when the experts average 384 rows or more.
+// Three tile configurations, all 8 waves x 256 weight rows but the last:
+// BM = 128 with K steps of 64 and three 48 KB stages; BM = 256 with K steps
+// of 32 and four 32 KB stages (fewer operand bytes per flop, larger jobs);
+// BM = 64 with K steps of 64 against 128 weight rows on 4 waves, three 24 KB
+// stages, so two workgroups share a CU.  Down always uses the first; gate/up
+// uses the second when the experts average 384 rows or more and the third
+// when the tile list leaves at most 16 rows per entry.  A tile whose M-tile
+// holds fewer than BM real rows runs the MFMAs of the 64-row parts that hold
+// them only.
 //
-// Gate/up: B = 128 rows of w1 and the same 128 rows of w3, so each wave holds
-// the gate and up sums of the same outputs and applies SwiGLU in registers; h
-// is written row-major [sorted row, I] through an LDS-staged, coalesced store.
+// Gate/up: B = 128 rows of w1 and the same 128 rows of w3 (64 and 64 in the
+// 4-wave tile), so each wave holds the gate and up sums of the same outputs
+// and applies SwiGLU in registers; h is written row-major [sorted row, I]
+// through an LDS-staged, coalesced store.
 // Down: B = 256 rows of w2 over one K segment; the gate weight multiplies the
 // fp32 sums before the store of the partial y[segment].
 //
