@@ -108,8 +108,9 @@ def test_forward_f16_matches_fp64_golden(budget, path, monkeypatch):
 
 @pytest.mark.parametrize("t,h,i", [(64, 4096, 14336), (2048, 512, 1024)])
 def test_forward_f16_large_shapes(t, h, i):
-    """fp16 at the Mixtral layer shape (weight-streaming GEMMs) and at T=2048
-    (the tiled GEMMs with 256-row gate/up tiles)."""
+    """fp16 at the Mixtral layer shape (the tiled GEMMs with the 64-row gate/up
+    tile) and at T=2048 (256-row gate/up tiles, the last tile of each expert
+    running 1-4 of its 64-row parts)."""
     _say(f"forward fp16 t={t} h={h} i={i}")
     out, golden = _forward_f16(t, 8, h, i, 8, 43)
     err = op1_ref.rel_l2(out.cpu().float(), golden)
