@@ -70,11 +70,14 @@ class _Scratch:
     partials, the int32 argmax vector, and the pinned host word the KV commit
     writes num_accepted into (created on first use)."""
 
-    __slots__ = ("partials", "argmax", "note", "note_np", "note_dev")
+    __slots__ = ("partials", "argmax", "partials_ptr", "argmax_ptr", "note", "note_np",
+                 "note_dev")
 
     def __init__(self, n: int, device):
         self.partials = argmax_workspace(n, device)
         self.argmax = torch.empty(n, dtype=torch.int32, device=device)
+        self.partials_ptr = self.partials.data_ptr()
+        self.argmax_ptr = self.argmax.data_ptr()
         self.note = None
 
     def host_count(self) -> int:
@@ -262,9 +265,11 @@ def fused_verify_commit(
     else:
         raise TypeError(f"target_logits must be float32 or bfloat16, got {target_logits.dtype}")
     n, v = target_logits.shape
-    dev = target_logits.device
+    # the CUDA device index: a plain int keys the per-device caches and
+    # selects the device below (cheaper per call than torch.device objects)
+    dev = target_logits.get_device()
     tokens = tree_tokens
-    if tokens.device != dev or tokens.dtype != torch.int64 or not tokens.is_contiguous():
+    if tokens.get_device() != dev or tokens.dtype != torch.int64 or not tokens.is_contiguous():
         tokens = tokens.to(device=dev, dtype=torch.int64).contiguous()
     if tokens.numel() != n:
         raise ValueError("tree_tokens must have one entry per node")
@@ -277,7 +282,8 @@ def fused_verify_commit(
     p_slots = out.data_ptr()
     p_toks, p_result = p_slots + 8 * n, p_slots + 16 * n
     stream = _capi.stream_of(dev)
-    c_start, c_count, c_list = ptr(csr), ptr(csr) + 4 * n, ptr(csr) + 8 * n
+    c_start = csr.data_ptr()
+    c_count, c_list = c_start + 4 * n, c_start + 8 * n
     if temperature != 0.0:
         q = draft_probs
         if (q is None or not q.is_cuda or q.dtype != torch.float32 or q.dim() != 2
@@ -298,7 +304,7 @@ def fused_verify_commit(
         ws = _scratch(n, dev)
         args = (ptr(target_logits), dtype, n, v, target_logits.stride(0), ptr(tokens), c_start,
                 c_count, c_list, num_edges, max_depth, 1 if rep_penalty != 1.0 else 0,
-                ptr(ws.argmax), p_slots, p_toks, p_result, ptr(ws.partials), stream)
+                ws.argmax_ptr, p_slots, p_toks, p_result, ws.partials_ptr, stream)
         if _fast is not None:
             check(_fast.argmax_walk(*args), "tm_op4_argmax_walk")
         else:
