@@ -525,6 +525,59 @@ def test_tiled_gemms_ragged_column_blocks(t, e, i, budget, monkeypatch):
     assert err <= REL_L2_TOL
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_tiled_gate_up_partial_tiles(dtype):
+    """The 256-row gate/up tile on a hand-made layout whose experts end in
+    tiles of 1, 100, 150, 250 and 11 rows (1, 2, 3, 4 and 1 of the 64-row
+    parts run their MFMAs): every sorted row of h meets a float32 torch
+    evaluation of silu(x w1^T) * (x w3^T), and no row past the slots is
+    written."""
+    from treemoe_spec_amd import _capi
+
+    _say(f"tiled gate/up partial tiles {dtype}")
+    t, h, i = 1024, 512, 1024
+    counts = [257, 356, 150, 250, 1035]  # 2T slots over E = 5 experts: 2T >= 384 E
+    e = len(counts)
+    assert sum(counts) == 2 * t and 2 * t >= 384 * e
+    g = torch.Generator().manual_seed(97)
+    x = torch.randn(t, h, generator=g).to(dtype)
+    w1 = (torch.randn(e, i, h, generator=g) * 0.05).to(dtype)
+    w3 = (torch.randn(e, i, h, generator=g) * 0.05).to(dtype)
+    slots = torch.randperm(2 * t, generator=g).to(torch.int32)
+    offsets = [0]
+    for c in counts:
+        offsets.append(offsets[-1] + c)
+    tiles = []
+    for k, c in enumerate(counts):
+        for r0 in range(0, c, 64):
+            tiles.append([k, offsets[k] + r0, min(64, c - r0), 0])
+    dev = torch.device("cuda")
+    xd, w1d, w3d = x.to(dev), w1.to(dev), w3.to(dev)
+    slots_d = slots.to(dev)
+    offsets_d = torch.tensor(offsets, dtype=torch.int32, device=dev)
+    tiles_d = torch.tensor(tiles, dtype=torch.int32, device=dev)
+    # one spare row past the 2T slots: it must keep its fill value
+    hd = torch.full((2 * t + 1, i), 7.0, dtype=dtype, device=dev)
+    code = _capi.TM_DTYPE_F16 if dtype == torch.float16 else _capi.TM_DTYPE_BF16
+    _capi.call("tm_op1_prefill_gemm1", xd.data_ptr(), w1d.data_ptr(), w3d.data_ptr(),
+               hd.data_ptr(), slots_d.data_ptr(), offsets_d.data_ptr(), tiles_d.data_ptr(),
+               len(tiles), t, h, i, e, code, _capi.stream_of(dev))
+    torch.cuda.synchronize()
+    out = hd.float().cpu()
+    assert torch.all(out[2 * t] == 7.0)
+    xf, w1f, w3f = x.float(), w1.float(), w3.float()
+    for k, c in enumerate(counts):
+        rows = slice(offsets[k], offsets[k + 1])
+        tok = slots[rows].long() >> 1
+        a = xf[tok] @ w1f[k].T
+        b = xf[tok] @ w3f[k].T
+        ref = (a / (1.0 + torch.exp(-a))) * b
+        err = (out[rows] - ref).norm() / ref.norm()
+        worst = ((out[rows] - ref).abs().amax(1) / ref.abs().amax(1)).max()
+        _say(f"  expert {k} rows {c}: rel_l2={err:.2e} worst row {worst:.2e}")
+        assert err <= 1e-2 and worst <= 2e-2
+
+
 def test_tiled_down_gemm_segment_counts_agree(monkeypatch):
     """The tiled path at a small shape takes 4 K segments for the down GEMM;
     forced back to 2 it must give the same layer up to fp32 summation order,
