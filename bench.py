@@ -73,6 +73,24 @@ def events_time_ms(fn, reps: int) -> float:
     return median(step_times_ms(fn, reps))
 
 
+def device_time_ms(fn, reps: int, spin_cycles: int = 200_000) -> float:
+    """Median device time of fn() over `reps` calls, each queued behind a GPU
+    spin (torch.cuda._sleep) long enough for the host to issue all of the
+    call's launches first: host-side launch cost then opens no gaps between
+    its kernels.  One HIP event pair per call on the current stream."""
+    import torch
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(reps)]
+    for s, e in ev:
+        torch.cuda._sleep(spin_cycles)
+        s.record()
+        fn()
+        e.record()
+    ev[-1][1].synchronize()
+    return median([s.elapsed_time(e) for s, e in ev])
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -366,7 +384,8 @@ def secondary(m, inp2, args) -> dict:
     ms = events_time_ms(step, reps)
     # device side alone: the two C-ABI calls with the CSR, tables and outputs
     # already resident (the host glue above builds the CSR and reads back
-    # num_accepted, as the reference does)
+    # num_accepted, as the reference does), each call queued behind a GPU spin
+    # so that the host's launch cost is not timed
     from treemoe_spec_amd import _capi
 
     dev = logits.device
@@ -394,7 +413,7 @@ def secondary(m, inp2, args) -> dict:
 
     for _ in range(3):
         device_step()
-    dev_ms = events_time_ms(device_step, max(reps, 50))
+    dev_ms = device_time_ms(device_step, max(reps, 50))
     # cold: a 512 MB write before each timed call evicts the 256 MB Infinity
     # Cache and the L2s, so the logits and KV rows come from HBM
     flush = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
@@ -435,7 +454,7 @@ def secondary(m, inp2, args) -> dict:
 
     for _ in range(3):
         sample_step()
-    sample_ms = events_time_ms(sample_step, max(reps, 50))
+    sample_ms = device_time_ms(sample_step, max(reps, 50))
     nodes_visited = int(result[1]) + 1
     pen_logits = logits.clone()
     prev = torch.randint(0, v, (512,), generator=g).cuda()
@@ -449,7 +468,7 @@ def secondary(m, inp2, args) -> dict:
 
     for _ in range(3):
         penalty_step()
-    pen_ms = events_time_ms(penalty_step, max(reps, 50))
+    pen_ms = device_time_ms(penalty_step, max(reps, 50))
     out["config4_op4_sampling"] = {
         "us_sample_walk": round(sample_ms * 1e3, 2), "nodes_visited": nodes_visited,
         # per visited node: the row's softmax (3 logit passes) and the residual
@@ -463,8 +482,9 @@ def tree_attention_secondary(reps: int) -> dict:
     """The verification forward's attention at the config-4 cache shape: a
     64-node tree (random parents, depth <= 8), 32 query heads over 8 KV heads,
     head dim 128, page 16, 4096 committed positions, one layer.  Device time
-    of the C-ABI call (mask packed and tables resident), the CPU oracle on a
-    bounded sample beside it."""
+    of the C-ABI call (mask packed and tables resident), the reference's torch
+    composition of the same step on this GPU, and the CPU oracle on a bounded
+    sample beside them."""
     import ctypes
 
     import torch
@@ -518,6 +538,26 @@ def tree_attention_secondary(reps: int) -> dict:
                  + 2 * 2 * n * kvh * hd * 2      # tree K and V read, and stored to scratch
                  + 2 * n * hq * hd * 2)          # q in, context out
     flops = 4 * n * hq * (seq + n) * hd          # QK^T and PV over every key, masked or not
+    # the reference's own torch composition on this GPU (mixtral.py:208-250):
+    # write_tree, gather_with_tail, the boolean mask, SDPA with enable_gqa
+    import torch.nn.functional as F
+
+    def torch_composition():
+        kv.write_tree(0, k, v)
+        fk, fv = kv.gather_with_tail(0, k, v)
+        pre = fk.shape[0] - n
+        full = torch.zeros(n, pre + n, dtype=torch.bool, device="cuda")
+        full[:, :pre] = True
+        full[:, pre:] = mask
+        o = F.scaled_dot_product_attention(
+            q.transpose(0, 1).unsqueeze(0), fk.transpose(0, 1).unsqueeze(0),
+            fv.transpose(0, 1).unsqueeze(0), attn_mask=full[None, None], scale=hd ** -0.5,
+            enable_gqa=True)
+        return o.transpose(1, 2).contiguous().reshape(n, hq * hd)
+
+    for _ in range(3):
+        torch_composition()
+    torch_ms = events_time_ms(torch_composition, 20)
     # CPU: the oracle (float32 restatement of gather + mask + SDPA) on the host
     kc_cpu, vc_cpu = kv.k.cpu(), kv.v.cpu()
     qc, kt, vt, mc = q.cpu(), k.cpu(), v.cpu(), mask.cpu()
@@ -531,6 +571,7 @@ def tree_attention_secondary(reps: int) -> dict:
             "pct_mfma_peak": round(100 * flops / (dev_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
                                    2),
             "bytes_alg": bytes_alg, "flops": flops,
+            "us_torch_reference_composition": round(torch_ms * 1e3, 2),
             "cpu_oracle_ms": round(cpu_ms, 2), "cpu_threads": torch.get_num_threads()}
 
 
