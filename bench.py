@@ -363,6 +363,7 @@ def secondary(m, inp2, args) -> dict:
                                   "pct_hbm_peak": round(100 * b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
         del w1, w2, w3
     out["config2_tensor_parallel_share"] = shares
+    out["config2_torch_composition"] = torch_composition_op1(m, inp2, reps)
     log("secondary op4 config 4")
     w = op4_workload(n=64, vocab=32000, max_depth=8, seed=3)
     cfg = MixtralConfig()
@@ -476,6 +477,44 @@ def secondary(m, inp2, args) -> dict:
         "us_rep_penalty_512_prev_tokens": round(pen_ms * 1e3, 2)}
     out["config4_tree_attention"] = tree_attention_secondary(reps)
     return out
+
+
+def torch_composition_op1(m, inp, reps: int) -> dict:
+    """Config 2's expert FFN and combine as plain torch ops on this GPU (one
+    F.linear per expert and projection, i.e. hipBLASLt, SiLU, the gate
+    weights and an index_add), with this build's routing computed and the
+    per-expert row lists built before the timed region: a vendor-library
+    point of comparison for tree_moe_forward, not the reference's kernels."""
+    import torch
+    import torch.nn.functional as F
+
+    x, w1, w2, w3 = inp.x, inp.w1, inp.w2, inp.w3
+    t, h = x.shape
+    e = w1.shape[0]
+    r = m.route_experts(x, inp.router, inp.accept, inp.budget, w1.shape[1])
+    ids = r.topk_ids.reshape(-1)
+    gates = r.gates_flat.reshape(-1)
+    groups = []
+    for k in range(e):
+        slots = torch.nonzero(ids == k).flatten()
+        if slots.numel():
+            groups.append((k, slots // 2, gates[slots].unsqueeze(1)))
+
+    def step():
+        y = torch.zeros(t, h, dtype=torch.float32, device=x.device)
+        for k, tok, g in groups:
+            xe = x[tok]
+            he = F.silu(F.linear(xe, w1[k])) * F.linear(xe, w3[k])
+            y.index_add_(0, tok, F.linear(he, w2[k]).float() * g)
+        return y.to(x.dtype)
+
+    ref = step().float()
+    ours = m.tree_moe_forward(x, w1, w2, w3, inp.router, inp.accept, inp.budget).float()
+    for _ in range(3):
+        step()
+    ms = events_time_ms(step, reps)
+    return {"us": round(ms * 1e3, 2),
+            "rel_l2_vs_tree_moe_forward": round(float((ref - ours).norm() / ref.norm()), 5)}
 
 
 def tree_attention_secondary(reps: int) -> dict:
