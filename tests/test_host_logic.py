@@ -363,3 +363,24 @@ def test_tiled_gate_up_tile_rule():
     assert m.tiled_gate_up_tile(2048, 8, tiles(2048, 8)) == "Tile<256, 32, 4>"        # config 5
     assert m.tiled_gate_up_tile(32, 8, tiles(32, 8)) == "Tile<64, 64, 3, 128, 256>"
     assert m.tiled_gate_up_tile(128, 8, tiles(128, 8)) == "Tile<128, 64, 3>"
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with a message before
+    touching a device."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    proc = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"],
+                          capture_output=True, text=True, timeout=120, cwd=root)
+    assert proc.returncode == 2
+    assert "one GPU only" in proc.stderr
+
+
+def test_bench_median():
+    import bench
+
+    assert bench.median([3.0, 1.0, 2.0]) == 2.0
+    assert bench.median([4.0, 1.0, 3.0, 2.0]) == 2.5
