@@ -91,14 +91,91 @@ def device_time_ms(fn, reps: int, spin_cycles: int = 200_000) -> float:
     return median([s.elapsed_time(e) for s, e in ev])
 
 
-def cpu_model() -> str:
+def host_cpu() -> dict:
+    """What the host says about its CPU: /proc/cpuinfo's model name, family,
+    model and stepping numbers (some hosts give no model number in the
+    name), the logical CPUs and the ones this process may run on."""
+    info = {"model_name": platform.processor() or platform.machine()}
+    fields = {"model name": "model_name", "cpu family": "family", "model": "model",
+              "stepping": "stepping", "cpu MHz": "mhz"}
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if not line.strip():
+                break  # the first processor's block is enough
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in fields:
+                info[fields[key]] = val.strip()
     except OSError:
         pass
-    return platform.processor() or platform.machine()
+    info["logical_cpus"] = os.cpu_count()
+    try:
+        info["usable_cpus"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["usable_cpus"] = os.cpu_count()
+    return info
+
+
+def cpu_model() -> str:
+    c = host_cpu()
+    desc = c.get("model_name", "unknown")
+    if "family" in c:
+        desc += f" (family {c['family']}, model {c.get('model', '?')}, stepping " \
+                f"{c.get('stepping', '?')})"
+    return desc
+
+
+def _median_cpu_ms(fn, reps: int = 10, warmup: int = 2) -> tuple[float, int]:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return median(times) * 1e3, reps
+
+
+def cpu_path_timings() -> dict:
+    """The reference's CPU path at the two other shapes the baseline plan
+    names, through the torch restatement in oracle/ (same torch calls in the
+    same order as treemoe/ref): op1 at config 1 (T=64, H=1024, I=3584, E=8,
+    B=8; tree_moe_ref.py:102-130) and op4 at config 4 (greedy tree_verify,
+    verify_ref.py:35-103, then commit_tree at page 16, kv_cache.py:88-106:
+    N=64, V=32000 fp32 logits as the engine passes them, 32 layers x 8 KV
+    heads x 128, 4096 committed positions).  Median of 10 after 2 warm-ups."""
+    import torch
+
+    from oracle import op1_ref, op4_ref
+    from treemoe_spec_amd.workloads import op1_workload, op4_workload
+
+    inp = op1_workload("config1_cpu_small", device="cpu")
+    args = (inp.x, inp.w1, inp.w2, inp.w3, inp.router, inp.accept, inp.budget)
+    c1_ms, c1_reps = _median_cpu_ms(lambda: op1_ref.tree_moe_forward(*args))
+    del inp, args
+
+    w = op4_workload(n=64, vocab=32000, max_depth=8, seed=3)
+    logits = w.logits.float()
+    layers, kvh, hd, page, seq = 32, 8, 128, 16, 4096
+    n_scratch = (64 + page - 1) // page
+    pages = n_scratch + seq // page + 1
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(layers, pages, page, kvh, hd, generator=g).to(torch.bfloat16)
+    v = torch.randn(layers, pages, page, kvh, hd, generator=g).to(torch.bfloat16)
+    scratch = list(range(n_scratch))
+    table = (torch.randperm(pages - n_scratch, generator=g) + n_scratch).tolist()
+
+    def op4_step():
+        slots, _, _, num = op4_ref.tree_verify(logits, None, w.tokens, w.children)
+        commit = torch.cat([torch.zeros(1, dtype=torch.long), slots[:num]])
+        op4_ref.commit_tree(k, v, commit, scratch, table, seq)
+        return num
+
+    accepted = op4_step()
+    op4_ms, op4_reps = _median_cpu_ms(op4_step)
+    return {"config1_ms": round(c1_ms, 3), "config1_reps": c1_reps,
+            "op4_config4_ms": round(op4_ms, 3), "op4_config4_reps": op4_reps,
+            "op4_config4_accepted": accepted}
 
 
 def kernel_breakdown(m, inp, reps: int) -> dict:
@@ -191,7 +268,7 @@ def cpu_baseline(inp, budget_s: float, bytes_alg: int) -> dict:
             break
     times.sort()
     med = times[len(times) // 2]
-    return {
+    line = {
         "value": round(bytes_alg / med / 1e9, 3),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
@@ -199,9 +276,16 @@ def cpu_baseline(inp, budget_s: float, bytes_alg: int) -> dict:
         "sample": (f"{len(times)} full config-2 layers (T=64, H=4096, I=14336, E=8, B=8) "
                    f"through the torch CPU restatement of treemoe/ref/tree_moe_ref.py; "
                    f"median {med * 1e3:.1f} ms/layer; host CPU {cpu_model()}, "
-                   f"os.cpu_count()={threads}, torch threads {torch.get_num_threads()}"),
+                   f"os.cpu_count()={threads}, torch threads {torch.get_num_threads()}; "
+                   "config1_ms / op4_config4_ms: the same restatement at config 1 and "
+                   "op4 (tree_verify + commit_tree, page 16) at config 4, median of 10 "
+                   "after 2 warm-ups"),
         "ms_per_layer": round(med * 1e3, 3),
+        "host_cpu": host_cpu(),
+        "torch_threads": torch.get_num_threads(),
     }
+    line.update(cpu_path_timings())
+    return line
 
 
 def main():

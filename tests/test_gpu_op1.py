@@ -435,6 +435,20 @@ def test_masked_expert_weights_never_read(path, monkeypatch):
     assert not out.isnan().any()
 
 
+def _check_excluded_gates(routing, ids, gates_before, cold, info):
+    """As the reference's exclude_experts does (op1_tree_moe.py:630), the
+    excluded slots' gates are zero in gates_flat afterwards, every other gate
+    is unchanged, and the returned host gates are the values from before."""
+    cold_mask = torch.isin(ids, torch.tensor(cold, device=ids.device))
+    after = routing.gates_flat
+    assert bool((after[cold_mask] == 0).all())
+    assert torch.equal(after[~cold_mask], gates_before[~cold_mask])
+    for e, toks, gts in info:
+        slots = (ids == e).nonzero().flatten()
+        assert torch.equal(gts, gates_before[slots].float().cpu())
+        assert torch.equal(toks, (slots // 2).cpu())
+
+
 def test_exclude_experts_hybrid_matches_full(monkeypatch):
     """Weight-streaming GEMMs (test_exclude_experts_tiled_path covers the tiled
     ones)."""
@@ -447,9 +461,12 @@ def test_exclude_experts_hybrid_matches_full(monkeypatch):
     full = m.tree_moe_forward(*dev, 4).clone()
     routing = m.route_experts(dev[0], dev[4], dev[5], 4, 1024)
     cold = routing.expert_ids()[:2]
+    ids = routing.topk_ids.reshape(-1).clone()
+    gates_before = routing.gates_flat.clone()
     info = routing.exclude_experts(cold)
     assert [e for e, _, _ in info] == cold
     assert not set(routing.expert_ids()) & set(cold)
+    _check_excluded_gates(routing, ids, gates_before, cold, info)
     hybrid = m.tree_moe_forward(*dev, 4, routing=routing).float().cpu()
     for e, toks, gts in info:
         xe = x[toks].double()
@@ -607,7 +624,10 @@ def test_exclude_experts_tiled_path():
     full = m.tree_moe_forward(*dev, budget).clone()
     routing = m.route_experts(dev[0], dev[4], dev[5], budget, 1024)
     cold = routing.expert_ids()[:2]
+    ids = routing.topk_ids.reshape(-1).clone()
+    gates_before = routing.gates_flat.clone()
     info = routing.exclude_experts(cold)
+    _check_excluded_gates(routing, ids, gates_before, cold, info)
     hybrid = m.tree_moe_forward(*dev, budget, routing=routing).float().cpu()
     for e, toks, gts in info:
         xe = x[toks].double()

@@ -239,7 +239,10 @@ def test_commit_count_word_across_calls(monkeypatch, binding):
 
     n, seq0 = 64, 100
     kv = _kv_setup(2, 2, 16, 16, 80, seq0, n, 5, torch.bfloat16)
-    ws = op4._scratch(n, torch.device("cuda", torch.cuda.current_device()))
+    from treemoe_spec_amd import _capi
+
+    dev = torch.cuda.current_device()
+    key = op4._scratch_key(n, dev, _capi.stream_of(dev))
     nums = []
     for call, seed in enumerate((11, 12, 13, 14, 15, 16)):
         if call == 3:
@@ -252,11 +255,39 @@ def test_commit_count_word_across_calls(monkeypatch, binding):
         assert kv.seq_len == before + ref_num + 1, (call, seed)
         torch.cuda.synchronize()
         assert int(res.num_accepted) == ref_num
-        key = next(k for k in op4._scratch_cache if k[0] == n)
         ws = op4._scratch_cache[key]
         assert ws.note_dev != 0 and int(ws.note_np[0]) == ref_num
         nums.append(ref_num)
     assert len(set(nums)) > 1, "the seeds should give different path lengths"
+
+
+def test_two_streams_do_not_share_partials():
+    """Two kv=None calls with the same N on two streams, the first queued
+    behind a GPU spin so that the second is issued while the first's kernels
+    still wait: each returns its own tree's accepted path (the row partials
+    and argmax vector are per stream)."""
+    _say("two streams, kv=None, same N")
+    op4 = _op4()
+    from treemoe_spec_amd.workloads import op4_workload
+
+    n = 64
+    ws = [op4_workload(n=n, vocab=4096, max_depth=8, seed=s) for s in (21, 22)]
+    refs = [op4_ref.tree_verify(w.logits.float(), None, w.tokens, w.children) for w in ws]
+    assert refs[0][3] != refs[1][3] or not torch.equal(refs[0][0], refs[1][0])
+    ins = [(w.logits.cuda(), w.tokens.cuda(), w.parent.cuda()) for w in ws]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    res = [None, None]
+    with torch.cuda.stream(streams[0]):
+        torch.cuda._sleep(2_000_000)
+        res[0] = op4.fused_verify_commit(ins[0][0], None, ins[0][1], ins[0][2], ws[0].children)
+    with torch.cuda.stream(streams[1]):
+        res[1] = op4.fused_verify_commit(ins[1][0], None, ins[1][1], ins[1][2], ws[1].children)
+    torch.cuda.synchronize()
+    for r, (slots, toks, bonus, num) in zip(res, refs):
+        assert torch.equal(r.accepted_slots.cpu(), slots)
+        assert torch.equal(r.accepted_tokens.cpu(), toks)
+        assert int(r.bonus_token) == bonus and int(r.num_accepted) == num
 
 
 def test_config4_planted_path_accepted():

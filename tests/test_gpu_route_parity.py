@@ -16,19 +16,18 @@ different bf16 values.  The test therefore requires:
     (H - 1) 2^-24 sum |x_k w_k| of the exact sum; rounding adds one ulp).
     Exact device logits come from the C oracle, which reproduces the device's
     gates bit for bit (asserted);
-  * topk_ids identical to torch's, except on rows explained by
-    - an exact tie: torch's gates at the two picks are equal in value at each
-      position, so the rows differ only in which of two exactly equal experts
-      is taken.  torch.topk orders exact ties in an implementation-defined
-      way (it varies with the host CPU); the device takes the lower expert id,
-      as the reference's own routing kernel does with its first-occurrence
-      argmax (op1_tree_moe.py:226-232);
-    - or a logit difference: the row itself has a differing logit, or the
-      keep set differs (then some logit differs and the keep order had a
-      near-tie);
+  * the keep set identical to torch's, and topk_ids identical to torch's on
+    every row except exact ties: torch's gates at the two picks are equal in
+    value at each position, so the rows differ only in which of two exactly
+    equal experts is taken.  torch.topk orders exact ties in an
+    implementation-defined way (it varies with the host CPU); the device
+    takes the lower expert id, as the reference's own routing kernel does
+    with its first-occurrence argmax (op1_tree_moe.py:226-232).  A row whose
+    ids differ because a bf16 logit differs fails the test (the rule is in
+    tests/route_parity.py, and tests/test_route_parity_rule.py shows that a
+    planted near-tie flip fails it);
   * renormalised gates within 1e-5 (relative) of torch's on every row whose
-    logits are identical and whose ids are identical or differ only by an
-    exact tie (2e-2 where a logit differs by a bf16 ulp).
+    logits are identical (2e-2 where a logit differs by a bf16 ulp).
 The counts are printed (run with -s) and recorded in the design notes.
 """
 
@@ -41,6 +40,7 @@ import torch.nn.functional as F
 
 from oracle import op1_ref, oracle_c
 from tests.conftest import bf16_bits
+from tests.route_parity import classify_id_rows, require_bit_exact
 
 pytestmark = pytest.mark.gpu
 
@@ -111,34 +111,17 @@ def test_ids_match_torch_router(name, t, h, e, budget, seed, bias, objective, ac
     assert bool((gap <= bound).all()), "a device logit is off torch's by more than rounding"
     ulps = gap / _ulp(big).double()
     rows = (ids_d != ids_t).any(1)
-    tie_rows, logit_rows = [], []
-    for r in rows.nonzero().flatten().tolist():
-        gd = gates_t[r, ids_d[r]]
-        gt = gates_t[r, ids_t[r]]
-        if keep_d == keep_t and torch.equal(gd, gt):
-            # an exact tie: the device's pick is the lowest id among the tied
-            for k in range(2):
-                if int(ids_d[r, k]) != int(ids_t[r, k]):
-                    tied = [j for j in keep_d if gates_t[r, j] == gd[k]
-                            and j not in ids_d[r, :k].tolist()]
-                    assert int(ids_d[r, k]) == min(tied), (r, k, tied)
-            tie_rows.append(r)
-            continue
-        assert keep_d != keep_t or bool(differ[r].any()), (
-            f"row {r}: ids {ids_d[r].tolist()} vs torch {ids_t[r].tolist()} with identical "
-            "logits and keep set and unequal gates")
-        logit_rows.append(r)
-    # gates: tight where the row's logits are identical; where a logit differs
-    # by a bf16 ulp (2^-8 relative) the softmax moves by about as much
-    same = ~differ.any(1)
-    same[logit_rows] = False
-    torch.testing.assert_close(w_d[same], w_t[same], rtol=1e-5, atol=1e-7)
-    near = differ.any(1)
-    near[logit_rows] = False
-    torch.testing.assert_close(w_d[near], w_t[near], rtol=2e-2, atol=1e-4)
+    tie_rows, logit_rows = classify_id_rows(ids_d, ids_t, gates_t, keep_d, keep_t, differ)
     print(f"  logits differing from torch's: {int(differ.sum())} of {differ.numel()} "
           f"(at most {float(ulps.max()):.0f} bf16 ulp); "
           f"keep set {'differs' if keep_d != keep_t else 'identical'}; "
           f"rows with different ids: {int(rows.sum())} of {t} "
           f"({len(tie_rows)} exact ties, {len(logit_rows)} from a logit difference)",
           flush=True)
+    require_bit_exact(keep_d, keep_t, logit_rows)
+    # gates: tight where the row's logits are identical; where a logit differs
+    # by a bf16 ulp (2^-8 relative) the softmax moves by about as much
+    same = ~differ.any(1)
+    torch.testing.assert_close(w_d[same], w_t[same], rtol=1e-5, atol=1e-7)
+    near = differ.any(1)
+    torch.testing.assert_close(w_d[near], w_t[near], rtol=2e-2, atol=1e-4)

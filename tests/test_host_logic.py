@@ -132,6 +132,42 @@ def test_children_csr_packing():
         _children_csr([[1]], 4, "cpu")
 
 
+def test_cached_csr_checks_the_node_count_on_a_hit():
+    """The same children list passed again with another N is rejected, not
+    served from the cache at offsets sized for the first N."""
+    from treemoe_spec_amd.kernels import op4_commit as o
+
+    children = [[1, 2], [3], [], []]
+    csr, edges = o._cached_csr(children, 4, "cpu")
+    again, _ = o._cached_csr(children, 4, "cpu")
+    assert again is csr and edges == 3
+    with pytest.raises(ValueError, match="list 8 nodes, got 4"):
+        o._cached_csr(children, 8, "cpu")
+    with pytest.raises(ValueError, match="list 3 nodes, got 4"):
+        o._cached_csr(children, 3, "cpu")
+
+
+def test_op4_scratch_key_separates_streams_and_threads():
+    """The greedy path's internal buffers are keyed by stream and host thread:
+    a kv=None call returns with its kernels still queued, so a call on a
+    second stream must not share its partials, and each thread reads its own
+    count word."""
+    import threading
+
+    from treemoe_spec_amd.kernels import op4_commit as o
+
+    k1 = o._scratch_key(64, 0, 0x1000)
+    assert k1 == o._scratch_key(64, 0, 0x1000)
+    assert k1 != o._scratch_key(64, 0, 0x2000)      # another stream
+    assert k1 != o._scratch_key(64, 1, 0x1000)      # another device
+    assert k1 != o._scratch_key(32, 0, 0x1000)      # another tree size
+    other = []
+    th = threading.Thread(target=lambda: other.append(o._scratch_key(64, 0, 0x1000)))
+    th.start()
+    th.join()
+    assert other[0] != k1                           # another host thread
+
+
 def test_kv_cache_bookkeeping_page16():
     from treemoe_spec_amd.kv_cache import MixtralConfig, PagedKVCache
 

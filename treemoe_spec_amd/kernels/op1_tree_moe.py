@@ -319,13 +319,15 @@ class Routing:
     def exclude_experts(self, expert_ids) -> list[tuple[int, torch.Tensor, torch.Tensor]]:
         """Drop these experts from the device pass and return
         [(expert, token_idx, gates)] host tensors for a host-side FFN
-        (reference :598-638).  Their GEMM tiles and reference blocks are
+        (reference :598-638).  As in the reference, their slots' gates in
+        ``gates_flat`` are zeroed, their GEMM tiles and reference blocks are
         masked and their partial rows zeroed, so the fixed-order combine adds
         exact zeros for them."""
         picked: list[tuple[int, torch.Tensor, torch.Tensor]] = []
         offsets = self.expert_offsets.tolist()
         drop = []
         rows = []
+        cold_slots = []
         for e in expert_ids:
             e = int(e)
             lo, hi = offsets[e], offsets[e + 1]
@@ -335,8 +337,10 @@ class Routing:
             picked.append((e, (slots // 2).cpu(), self.gates_flat[slots].float().cpu()))
             drop.append(e)
             rows.append(torch.arange(lo, hi, device=slots.device))
+            cold_slots.append(slots)
         if not picked:
             return picked
+        self.gates_flat[torch.cat(cold_slots)] = 0.0
         drop_t = torch.tensor(drop, device=self.tiles.device)
         tile_e = self.tiles[:, 0]
         self.tiles[:, 0] = torch.where(torch.isin(tile_e.long(), drop_t),

@@ -31,6 +31,7 @@ the random stream).  One launch, ``tm_op4_sample_walk``.
 from __future__ import annotations
 
 import ctypes
+import threading
 import time
 from dataclasses import dataclass
 
@@ -65,10 +66,14 @@ def argmax_workspace(n: int, device) -> torch.Tensor:
 
 
 class _Scratch:
-    """Per (N, device) internal buffers, reused by every call on that device
-    (stream-ordered, like the reference's workspaces): the argmax row
-    partials, the int32 argmax vector, and the pinned host word the KV commit
-    writes num_accepted into (created on first use)."""
+    """Internal buffers of the greedy path for one (N, device, stream, host
+    thread): the argmax row partials, the int32 argmax vector, and the pinned
+    host word the KV commit writes num_accepted into (created on first use).
+    Calls on one stream reuse them in stream order.  A call on another stream
+    gets its own: a call with kv=None returns while its kernels are still
+    queued, so a second stream would otherwise overwrite its partials.  A
+    call from another host thread gets its own too, so that each thread
+    reads the count word of its own commit."""
 
     __slots__ = ("partials", "argmax", "partials_ptr", "argmax_ptr", "note", "note_np",
                  "note_dev")
@@ -121,8 +126,15 @@ def _read_count(ws: _Scratch, result: torch.Tensor) -> int:
 _scratch_cache: dict[tuple, _Scratch] = {}
 
 
-def _scratch(n: int, device) -> _Scratch:
-    key = (n, device)
+def _scratch_key(n: int, device: int, stream: int) -> tuple:
+    return (n, device, stream, threading.get_ident())
+
+
+def _scratch(n: int, device: int, stream: int) -> _Scratch:
+    """The buffers of (N, device index, raw stream handle, calling thread),
+    allocated on first use while that stream is current, so that torch's
+    allocator orders their reuse on it."""
+    key = _scratch_key(n, device, stream)
     ws = _scratch_cache.get(key)
     if ws is None:
         if len(_scratch_cache) > 16:
@@ -187,7 +199,9 @@ _csr_cache: dict[tuple, tuple[list, torch.Tensor, int]] = {}
 
 
 def _cached_csr(children: list[list[int]], n: int, device) -> tuple[torch.Tensor, int]:
-    key = (id(children), device)
+    if len(children) != n:
+        raise ValueError(f"children must list {n} nodes, got {len(children)}")
+    key = (id(children), n, device)
     hit = _csr_cache.get(key)
     if hit is not None and hit[0] == children:
         return hit[1], hit[2]
@@ -301,7 +315,7 @@ def fused_verify_commit(
     else:
         if rep_penalty != 1.0:
             _apply_rep_penalty(target_logits, dtype, prev_tokens, rep_penalty, stream)
-        ws = _scratch(n, dev)
+        ws = _scratch(n, dev, stream)
         args = (ptr(target_logits), dtype, n, v, target_logits.stride(0), ptr(tokens), c_start,
                 c_count, c_list, num_edges, max_depth, 1 if rep_penalty != 1.0 else 0,
                 ws.argmax_ptr, p_slots, p_toks, p_result, ws.partials_ptr, stream)
@@ -316,7 +330,7 @@ def fused_verify_commit(
         # right behind the walk.  The count comes back through the pinned
         # word the commit writes (reference :267 reads it with a
         # device-to-host copy).
-        ws = _scratch(n, dev)
+        ws = _scratch(n, dev, stream)
         note = ws.host_count()
         if note:
             ws.note_np[0] = -1
