@@ -179,62 +179,32 @@ def cpu_path_timings() -> dict:
 
 
 def kernel_breakdown(m, inp, reps: int) -> dict:
-    """Median duration (ms) of each launch of one op1 step over `reps` steps,
-    events placed on the stream the library launches on (torch's current
-    stream)."""
+    """Median duration (ms) of each phase of one op1 step over `reps` steps:
+    tree_moe_forward's own launches (op1_tree_moe._forward), with an event
+    recorded after each phase on the stream the library launches on (torch's
+    current stream).  "route" is the router and, unless the gate/up launch
+    routes its own jobs, the bucketing; "gemm1" the gate/up launch."""
     import torch
-
-    from treemoe_spec_amd import _capi
 
     x, w1, w2, w3, router, accept, budget = (inp.x, inp.w1, inp.w2, inp.w3, inp.router,
                                              inp.accept, inp.budget)
     n, hidden = x.shape
     e, inter, _ = w1.shape
-    stream = _capi.stream_of(x.device)
-    tiled = m.uses_tiled_gemms(n, budget, e, inter)
     names = ["route", "gemm1", "gemm2", "combine"]
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(reps)]
     out = torch.empty_like(x)
     for r in range(reps):
+        marks = iter(ev[r][1:])
         ev[r][0].record()
-        routing = m.route_experts(x, router, accept, budget, inter)
-        ws = routing.ws
-        ev[r][1].record()
-        # the same launches as tree_moe_forward (op1_tree_moe.py): the tiled
-        # pair or the weight-streaming pair, then the combine
-        split = ws.split
-        if tiled:
-            split = m._tiled_split(n, budget, e, hidden, inter, ws)
-            _capi.call("tm_op1_prefill_gemm1", x.data_ptr(), w1.data_ptr(), w3.data_ptr(),
-                       ws.h.data_ptr(), routing.sorted_slots.data_ptr(),
-                       routing.expert_offsets.data_ptr(), routing.tiles.data_ptr(),
-                       routing.max_tiles, n, hidden, inter, e, _capi.TM_DTYPE_BF16, stream)
-            ev[r][2].record()
-            _capi.call("tm_op1_prefill_gemm2", ws.h.data_ptr(), w2.data_ptr(),
-                       ws.partial.data_ptr(), routing.gates_flat.data_ptr(),
-                       routing.sorted_slots.data_ptr(), routing.expert_offsets.data_ptr(),
-                       routing.tiles.data_ptr(), routing.max_tiles, split, n, hidden, inter, e,
-                       _capi.TM_DTYPE_BF16, stream)
-        else:
-            _capi.call("tm_op1_gemm1", x.data_ptr(), w1.data_ptr(), w3.data_ptr(),
-                       ws.h.data_ptr(), routing.sorted_slots.data_ptr(),
-                       routing.tiles.data_ptr(), routing.max_tiles, n, hidden, inter, e,
-                       _capi.TM_DTYPE_BF16, stream)
-            ev[r][2].record()
-            _capi.call("tm_op1_gemm2", ws.h.data_ptr(), w2.data_ptr(), ws.partial.data_ptr(),
-                       routing.gates_flat.data_ptr(), routing.sorted_slots.data_ptr(),
-                       routing.tiles.data_ptr(), routing.max_tiles, split, n, hidden, inter,
-                       e, _capi.TM_DTYPE_BF16, stream)
-        ev[r][3].record()
-        _capi.call("tm_op1_combine", ws.partial.data_ptr(), routing.slot_pos.data_ptr(),
-                   out.data_ptr(), n, hidden, split, _capi.TM_DTYPE_BF16, stream)
-        ev[r][4].record()
+        m._forward(x, w1, w2, w3, router, accept, budget, out, None, "mass",
+                   on_phase=lambda name, marks=marks: next(marks).record())
     torch.cuda.synchronize()
     res = {}
     for k, name in enumerate(names):
         res[name] = median([ev[r][k].elapsed_time(ev[r][k + 1]) for r in range(reps)])
-    res["tiled"] = tiled
-    res["max_tiles"] = routing.max_tiles
+    res["tiled"] = m.uses_tiled_gemms(n, budget, e, inter)
+    res["self_routed"] = m.self_routed(n, budget, e, inter)
+    res["max_tiles"] = m.compact_block_limit(2 * n, budget, m.TILE_M)
     return res
 
 
@@ -336,9 +306,10 @@ def main():
         fwd()
     bd = kernel_breakdown(m, inp, reps)
     tiled = bd.pop("tiled")
+    routed = bd.pop("self_routed")
     max_tiles = bd.pop("max_tiles")
-    gemm1_kernel = (f"tm_prefill_gemm1_kernel<{m.tiled_gate_up_tile(t, e, max_tiles)}>"
-                    if tiled else "tm_gemm1_kernel")
+    gemm1_kernel = (f"tm_prefill_gemm1{'_routed' if routed else ''}_kernel"
+                    f"<{m.tiled_gate_up_tile(t, e, max_tiles)}>" if tiled else "tm_gemm1_kernel")
     # algorithmic bytes per launch: one read of the active experts' weights
     # (w1 + w3 for gemm1, w2 for gemm2) plus the activation rows in (x); the
     # h and fp32-partial workspaces are not counted

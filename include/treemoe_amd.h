@@ -49,11 +49,12 @@ extern "C" {
 #define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
 #define TM_OP4_NOALLOC_MAX_NODES 2048  /* N limit of tm_op4_argmax_walk_noalloc */
 
-/* ABI version (major*10000 + minor*100 + patch): 4.0.0.  Version 2 added
+/* ABI version (major*10000 + minor*100 + patch): 4.1.0.  Version 2 added
  * num_edges to tm_op4_argmax_walk / tm_op4_sample_walk and softmax_argmax to
  * tm_op4_argmax_walk; version 3 added host_count to tm_op4_kv_commit;
  * version 4 added `dtype` (TM_DTYPE_BF16 or TM_DTYPE_F16) to the op1 entry
- * points that read or write 16-bit activations or weights. */
+ * points that read or write 16-bit activations or weights; 4.1 added
+ * tm_op1_prefill_gemm1_routed. */
 int tm_version(void);
 
 /* Human-readable text for a return code of any entry point. */
@@ -187,6 +188,29 @@ int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w3, void* h,
                          const int32_t* sorted_slots, const int32_t* expert_offsets,
                          const int32_t* tiles, int64_t max_tiles, int64_t T, int64_t H,
                          int64_t I, int64_t E, int dtype, void* stream);
+
+/*
+ * tm_op1_route_bucket and tm_op1_prefill_gemm1 in ONE launch, for few tokens:
+ * together with tm_op1_router_gates this replaces the routing and gate/up
+ * launches of the reference's tree_moe_forward (router op1_tree_moe.py:676-677,
+ * `_budget_bucket_fused_kernel` :159-297, `_moe_gemm1_kernel` :300-383, as
+ * launched at :771-781).  Every GEMM wave derives its own M-tile and rows
+ * from gates and accept (one token per lane, the bucketing's operations in
+ * the same floating-point order); one more workgroup writes every routing
+ * output of tm_op1_route_bucket (same arguments, same bits).  h is written as
+ * by tm_op1_prefill_gemm1 (row-major [2T, I], no expert masked), for
+ * tm_op1_prefill_gemm2 and tm_op1_combine with the routing outputs written
+ * here.  Requires 1 <= T <= 64, 2 <= E <= 16, max_blocks <= 256, and the
+ * shape rules of tm_op1_prefill_gemm1.
+ */
+int tm_op1_prefill_gemm1_routed(const void* x, const void* w1, const void* w3, void* h,
+                                const float* gates, const float* accept, int64_t T, int64_t H,
+                                int64_t I, int64_t E, int64_t budget, float tau, int objective,
+                                int64_t block_m, int64_t max_blocks, int64_t max_tiles,
+                                int64_t* topk_ids, float* gates_flat, int64_t* padded_slots,
+                                int64_t* block_expert_ids, int64_t* slot_to_row, float* demand,
+                                int32_t* expert_offsets, int32_t* sorted_slots,
+                                int32_t* slot_pos, int32_t* tiles, int dtype, void* stream);
 
 /*
  * Down projection for many rows per expert, MFMA-tiled over 128 rows x 256

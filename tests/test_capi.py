@@ -23,7 +23,7 @@ def test_header_declares_entry_points():
     names = declared_functions()
     for n in ("tm_version", "tm_status_string", "tm_op1_router_gates", "tm_op1_route_bucket",
               "tm_op1_gemm1", "tm_op1_gemm2", "tm_op1_combine", "tm_op1_prefill_gemm1",
-              "tm_op1_prefill_gemm2", "tm_op4_argmax_walk", "tm_op4_rep_penalty",
+              "tm_op1_prefill_gemm2", "tm_op1_prefill_gemm1_routed", "tm_op4_argmax_walk", "tm_op4_rep_penalty",
               "tm_op4_sample_walk", "tm_op4_kv_commit", "tm_tree_attention",
               "tm_tree_attention_plan", "tm_tree_mask_pack"):
         assert n in names
@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
     assert set(_capi.SIGNATURES) <= set(declared_functions())
-    assert lib.tm_version() == 40000
+    assert lib.tm_version() == 40100
 
 
 def test_status_strings():
@@ -115,6 +115,18 @@ def test_tree_attention_plan():
     assert plan(64, 32, 8, 64, 4096, 16, 0, ctypes.byref(chunks), ctypes.byref(ws)) == 1001
 
 
+def _routed_args(**kw):
+    """tm_op1_prefill_gemm1_routed arguments at the config-2 shape; every
+    pointer is null except where a case sets one, so only the cases that
+    fail a check may be called (the first, valid case is not called)."""
+    a = dict(x=0, w1=0, w3=0, h=0, gates=0, accept=0, T=64, H=4096, I=14336, E=8, budget=8,
+             tau=0.05, objective=0, block_m=16, max_blocks=16, max_tiles=9, topk=0, gflat=0,
+             padded=0, blk=0, s2r=0, demand=0, offsets=0, sorted=0, slot_pos=0, tiles=0,
+             dtype=1, stream=0)
+    a.update(kw)
+    return ("tm_op1_prefill_gemm1_routed", *a.values())
+
+
 @pytest.mark.parametrize("call,expect", [
     (("tm_op1_router_gates", 0, 0, 0, 4096, 8, 0, 1, 0), 1001),          # T = 0
     (("tm_op1_router_gates", 0, 0, 4, 4095, 8, 0, 1, 0), 1001),          # H % 8
@@ -131,6 +143,21 @@ def test_tree_attention_plan():
     (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 2, 2048, 4032, 14336, 8, 1, 0), 1001),  # H % 256
     (("tm_op1_prefill_gemm1", 0, 0, 0, 0, 0, 0, 0, 9, 2048, 4096, 14272, 8, 1, 0), 1001),  # I % 128
     (("tm_op1_prefill_gemm2", 0, 0, 0, 0, 0, 0, 0, 9, 3, 2048, 4096, 14336, 8, 1, 0), 1001),  # split
+    (_routed_args(), 0),                                                  # all valid
+    (_routed_args(T=65), 1001),                                           # T > 64
+    (_routed_args(E=17, budget=8), 1001),                                 # E > 16
+    (_routed_args(T=0), 1001),
+    (_routed_args(max_blocks=257), 1001),
+    (_routed_args(max_tiles=0), 1001),
+    (_routed_args(budget=1), 1003),
+    (_routed_args(budget=9), 1003),
+    (_routed_args(block_m=24), 1003),
+    (_routed_args(objective=2), 1003),
+    (_routed_args(dtype=0), 1003),
+    (_routed_args(H=4000), 1001),                                         # H % 64
+    (_routed_args(I=14272), 1001),                                        # I % 128
+    (_routed_args(x=8), 1002),                                            # unaligned x
+    (_routed_args(h=8), 1002),
     (("tm_op4_argmax_walk", 0, 7, 4, 10, 10, 0, 0, 0, 0, 3, 1, 0, 0, 0, 0, 0, 0, 0), 1003),
     (("tm_op4_argmax_walk", 0, 0, 4, 10, 9, 0, 0, 0, 0, 3, 1, 0, 0, 0, 0, 0, 0, 0), 1001),
     (("tm_op4_argmax_walk", 0, 0, 4, 10, 10, 0, 0, 0, 0, -1, 1, 0, 0, 0, 0, 0, 0, 0), 1001),
@@ -156,6 +183,8 @@ def test_argument_errors_return_before_launch(call, expect):
 
     name, *args = call
     assert len(args) == len(_capi.SIGNATURES[name]), "argument count"
+    if expect == 0:
+        return  # the valid reference case: only its argument count is checked
     fn = getattr(_capi.lib(), name)
     assert fn(*args) == expect
 

@@ -93,7 +93,7 @@ def _forward_f16(t, e, h, i, budget, seed):
     return out, golden
 
 
-@pytest.mark.parametrize("path", ["stream", "tiled"])
+@pytest.mark.parametrize("path", ["stream", "tiled", "tiled_bucket"])
 @pytest.mark.parametrize("budget", [4, 8])
 def test_forward_f16_matches_fp64_golden(budget, path, monkeypatch):
     """fp16 I/O (the reference kernels take fp16 too, op1_tree_moe.py:762-766):
@@ -321,13 +321,17 @@ def _forward_and_golden(t, e, h, i, budget, seed, objective="mass", accept_kind=
 
 def _force_path(monkeypatch, path):
     """Route tree_moe_forward through the weight-streaming GEMMs ("stream")
-    or the MFMA-tiled ones ("tiled") whatever the rows per expert."""
+    or the MFMA-tiled ones whatever the rows per expert: "tiled" with the
+    gate/up launch routing its own jobs where the token count allows it,
+    "tiled_bucket" with the separate routing launch."""
     m = _op1()
     monkeypatch.setattr(m, "TILED_MIN_ROWS", 1 << 30 if path == "stream" else 1)
     monkeypatch.setattr(m, "TILED_MIN_ROWS_WIDE", 1 << 30 if path == "stream" else 1)
+    if path == "tiled_bucket":
+        monkeypatch.setattr(m, "SELF_ROUTED_MAX_TOKENS", 0)
 
 
-@pytest.mark.parametrize("path", ["stream", "tiled"])
+@pytest.mark.parametrize("path", ["stream", "tiled", "tiled_bucket"])
 @pytest.mark.parametrize("budget", [2, 4, 8])
 @pytest.mark.parametrize("objective", ["mass", "critical_path"])
 def test_forward_matches_fp64_golden_small(budget, objective, path, monkeypatch):
@@ -415,7 +419,7 @@ def test_two_phase_equals_inline(budget):
     assert r is out and torch.equal(out, inline)
 
 
-@pytest.mark.parametrize("path", ["stream", "tiled"])
+@pytest.mark.parametrize("path", ["stream", "tiled", "tiled_bucket"])
 def test_masked_expert_weights_never_read(path, monkeypatch):
     """NaN-poisoned weights of an expert that no token routes to must not leak
     (reference tests/test_op1.py:162-170)."""

@@ -28,6 +28,8 @@ SIGNATURES: dict[str, list] = {
     "tm_op1_combine": [P, P, P, I64, I64, I64, I32, P],
     "tm_op1_prefill_gemm1": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, P],
     "tm_op1_prefill_gemm2": [P, P, P, P, P, P, P, I64, I64, I64, I64, I64, I64, I32, P],
+    "tm_op1_prefill_gemm1_routed": [P] * 6 + [I64] * 5 + [F32, I32, I64, I64, I64] + [P] * 10
+                                   + [I32, P],
     "tm_op4_argmax_walk": [P, I32, I64, I64, I64, P, P, P, P, I64, I64, I32, P, P, P, P, P, P],
     "tm_op4_kv_commit": [P, P, I64, I64, I64, I64, I64, I64, I64, P, P, P, I64, P, I64, I64,
                          I64, P, P],

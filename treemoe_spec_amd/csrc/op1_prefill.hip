@@ -41,6 +41,7 @@
 
 #include <algorithm>
 
+#include "op1_bucket.h"
 #include "tm_common.h"
 
 namespace {
@@ -415,6 +416,36 @@ __device__ __forceinline__ void gemm1_rows(const Stages& sb, const DmaLoad<C>& d
   gemm1_tile<C, MM, DT, NTB>(sb, d, nk, rows, p0, n0, I, h);
 }
 
+// One gate/up job: M-tile (expert e, sorted rows p0 .. p0 + rows) against
+// column block cb; d.ra and d.aoff (the A rows) are set by the caller.
+template <class C, int DT>
+__device__ __forceinline__ void gemm1_job(const Stages& sb, DmaLoad<C>& d,
+                                          const uint16_t* __restrict__ w1,
+                                          const uint16_t* __restrict__ w3,
+                                          uint16_t* __restrict__ h, int e, int p0, int rows,
+                                          bool single, int cb, int H, int I) {
+  const int n0 = cb * (C::PBN / 2);  // first h column of the block
+  const size_t ebase = (size_t)e * I * H;
+  d.rb0 = pbuf(w1 + ebase, (uint32_t)((size_t)I * H * 2));
+  d.rb1 = pbuf(w3 + ebase, (uint32_t)((size_t)I * H * 2));
+#pragma unroll
+  for (int i = 0; i < C::BLD; ++i) {
+    const int r = dma_row<C>(i);  // first half of the loads: w1 rows; second: the same w3 rows
+    d.boff[i] = (uint32_t)(n0 + (r & (C::PBN / 2 - 1))) * (uint32_t)H * 2u +
+                (uint32_t)dma_chunk<C>(r) * 16u;
+  }
+  // A tile with fewer than BM real rows (an expert's last) runs the MFMAs of
+  // its first ceil(rows / 64) 64-row quarters only; its A rows past `rows`
+  // are loaded as zeros without memory traffic.  An expert that takes one
+  // M-tile has its weights read by this job alone: they stream through with
+  // the non-temporal policy (a load-only probe streams 7.1 TB/s with it, 6.2
+  // without).  With several M-tiles the other jobs of the expert find them in
+  // L2, so those loads stay cached.
+  if (C::NT_WEIGHTS && single)
+    gemm1_rows<C, C::MT, DT, C::NT_WEIGHTS>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+  else gemm1_rows<C, C::MT, DT, false>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+}
+
 template <class C, int DT>
 __global__ void __launch_bounds__(C::NT)
 tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
@@ -434,13 +465,8 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   int e, p0, rows;
   bool single;
   if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows, &single)) return;
-  const int n0 = cb * (C::PBN / 2);  // first h column of the block
-
   DmaLoad<C> d;
   d.ra = pbuf(x, x_bytes);
-  const size_t ebase = (size_t)e * I * H;
-  d.rb0 = pbuf(w1 + ebase, (uint32_t)((size_t)I * H * 2));
-  d.rb1 = pbuf(w3 + ebase, (uint32_t)((size_t)I * H * 2));
 #pragma unroll
   for (int i = 0; i < C::ALD; ++i) {
     const int r = dma_row<C>(i);
@@ -448,22 +474,242 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
                                (uint32_t)dma_chunk<C>(r) * 16u
                          : kOOR;
   }
+  gemm1_job<C, DT>(sb, d, w1, w3, h, e, p0, rows, single, cb, H, I);
+}
+
+// ------------------------------------------------ gate/up, self-routed --
+// At few tokens the budget routing and bucketing run inside the gate/up
+// launch instead of in a launch of their own.  Launch index 0 runs the
+// routing phases of the routing kernel (tmb::bucket_phases, same code and
+// floating-point order) and writes every routing output (topk_ids,
+// gates_flat, the layouts, demand) for the down GEMM, the combine and the
+// Routing handle; indices 1 .. 7 exit, so GEMM job j = index - 8 keeps XCD
+// j % 8 (job_of).  Every wave of a GEMM workgroup derives its job from the
+// router gates by itself, one token per lane, with cross-lane operations only
+// (rr_job): no LDS and no barrier, one round of global loads (the gates), and
+// the same operations in the same order as the phases, so the same experts,
+// counts and rows.  Measured on MI355X against the routing launch, same box,
+// whole layer: config 2 440 against 445 us, config 3 (B = 4) 247 against
+// 252.5 us, the TP-2 and TP-4 shares 5 us faster each.  Tried first: every
+// GEMM workgroup running the LDS phases themselves (their barriers cost it
+// as much as the routing launch saved), and a per-wave view with one
+// reduction chain per expert in turn (~9 us per job instead of ~5).
+constexpr int kRrMaxTokens = 64;       // one token per lane
+constexpr int kRrMaxExperts = 16;      // gates of a token held in registers
+constexpr int kRvMaxBlocks = 256;      // reference padded blocks (the writer's LDS)
+constexpr int kRvLeaders = 8;          // launch indices before the GEMM jobs
+using RvShared = tmb::BucketSharedT<kRrMaxTokens, kRrMaxTokens * kRrMaxExperts, kRvMaxBlocks>;
+
+// Position of the j-th set bit (j from 0) of m, which has more than j.
+__device__ __forceinline__ int nth_set_bit(unsigned long long m, int j) {
+  int pos = 0;
 #pragma unroll
-  for (int i = 0; i < C::BLD; ++i) {
-    const int r = dma_row<C>(i);  // first half of the loads: w1 rows; second: the same w3 rows
-    d.boff[i] = (uint32_t)(n0 + (r & (C::PBN / 2 - 1))) * (uint32_t)H * 2u +
-                (uint32_t)dma_chunk<C>(r) * 16u;
+  for (int w = 32; w >= 1; w >>= 1) {
+    const unsigned long long low = m & ((1ull << w) - 1ull);
+    const int c = __popcll(low);
+    if (j >= c) {
+      j -= c;
+      pos += w;
+      m >>= w;
+    }
   }
-  // A tile with fewer than BM real rows (an expert's last) runs the MFMAs of
-  // its first ceil(rows / 64) 64-row quarters only; its A rows past `rows`
-  // are loaded as zeros without memory traffic.  An expert that takes one
-  // M-tile has its weights read by this job alone: they stream through with
-  // the non-temporal policy (a load-only probe streams 7.1 TB/s with it, 6.2
-  // without).  With several M-tiles the other jobs of the expert find them in
-  // L2, so those loads stay cached.
-  if (C::NT_WEIGHTS && single)
-    gemm1_rows<C, C::MT, DT, C::NT_WEIGHTS>(sb, d, H / C::PBK, rows, p0, n0, I, h);
-  else gemm1_rows<C, C::MT, DT, false>(sb, d, H / C::PBK, rows, p0, n0, I, h);
+  return pos;
+}
+
+// The kept experts (bit e) from the demand and criticality of every token
+// held in its lane (g: the lane's gates, zero past E or T), as the phases
+// compute them.
+template <int EM>
+__device__ __forceinline__ unsigned long long keep_set(const tmb::BucketArgs& a,
+                                                       const float (&g)[EM], bool tok,
+                                                       int lane) {
+  const int E = a.E;
+  const float a_ld = a.accept[tok ? lane : 0];
+  const float av = tok ? a_ld : 0.0f;
+  const bool critical = a.objective == TM_OBJECTIVE_CRITICAL_PATH;
+  // demand: the EM halving trees, level by level
+  float acc[EM];
+#pragma unroll
+  for (int e = 0; e < EM; ++e) {
+    float z = 0.0f;
+    const float p = av * g[e];
+    acc[e] = tok ? z + p : z;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+    for (int e = 0; e < EM; ++e) acc[e] = acc[e] + __shfl_xor(acc[e], off);
+  float d_mine = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EM; ++e) d_mine = lane == e ? acc[e] : d_mine;
+  float c_mine = 0.0f;
+  if (critical) {
+    tmb::Top2 u{-1, -1, 0.0f, 0.0f};
+#pragma unroll
+    for (int e = 0; e < EM; ++e)
+      if (e < E) u.offer(g[e], e);
+    float crit[EM];
+#pragma unroll
+    for (int e = 0; e < EM; ++e) {
+      const bool needed = tok && ((u.i1 == e) || ((u.i2 == e) && (av >= a.tau)));
+      crit[e] = needed ? fmaxf(-INFINITY, av) : -INFINITY;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+      for (int e = 0; e < EM; ++e) crit[e] = fmaxf(crit[e], __shfl_xor(crit[e], off));
+#pragma unroll
+    for (int e = 0; e < EM; ++e) c_mine = lane == e ? crit[e] : c_mine;
+  }
+  // keep set: lane = expert, as in the phases
+  {
+    const float d = lane < E ? d_mine : 0.0f;
+    const float c = (critical && lane < E) ? c_mine : 0.0f;
+    int rank = 0;
+#pragma unroll
+    for (int f = 0; f < EM; ++f) {
+      if (f < E) {
+        const float df = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(
+                                                       __builtin_bit_cast(int, acc[f])));
+        const float cf = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), f));
+        bool before;
+        if (critical && cf != c) {
+          before = cf > c;
+        } else if (df != d) {
+          before = df > d;
+        } else {
+          before = f < lane;
+        }
+        rank += before ? 1 : 0;
+      }
+    }
+    return __ballot(lane < E && rank < a.budget);
+  }
+}
+
+// The job of GEMM launch index l (M-tile of BM rows of one expert x column
+// block, job_of over the layer's real M-tiles) from the router gates, in one
+// wave: lane t holds token t's gates, EM >= E registers of them.  The expert
+// of each routed slot, each expert's count and compact offset, and the
+// M-tiles follow tmb::bucket_phases step by step:
+//   demand[e] = 0 + accept[t] gates[t, e] in lane t (0 past T), then the xor
+//   halving tree; crit[e] likewise with fmaxf (critical-path objective only);
+//   keep = ranks in the order (crit desc,) demand desc, e asc;
+//   masked top-2 per token, offered in expert order;
+//   the slots of expert e in slot order are the tokens whose top-2 holds e
+//   (the two picks differ), so each expert's rows are the set bits of one
+//   64-bit ballot, in token order, and its count that ballot's popcount.
+// The EM halving trees run interleaved and everything after them on wave-
+// uniform (scalar) values: a wave spends about a microsecond here beyond the
+// gates' load.  Returns false when l has no job.  `mask` is the expert's
+// token ballot and m0 the rank of the M-tile's first row among its rows.
+template <class C, int EM>
+__device__ __forceinline__ bool rr_job(const tmb::BucketArgs& a, int l, int ncol, int mt_max,
+                                       int* e_out, int* p0_out, int* rows_out, int* m0_out,
+                                       bool* single_out, int* cb_out,
+                                       unsigned long long* mask_out) {
+  const int lane = threadIdx.x & 63;
+  const int T = a.T, E = a.E;
+  const bool tok = lane < T;
+  float g[EM];
+  if ((E & 3) == 0 && (reinterpret_cast<uintptr_t>(a.gates) & 15) == 0) {
+#pragma unroll
+    for (int q = 0; q < EM / 4; ++q) {
+      const bool ok = tok && 4 * q < E;
+      const float4 v = *reinterpret_cast<const float4*>(a.gates + (ok ? lane * E + 4 * q : 0));
+      g[4 * q] = ok ? v.x : 0.0f;
+      g[4 * q + 1] = ok ? v.y : 0.0f;
+      g[4 * q + 2] = ok ? v.z : 0.0f;
+      g[4 * q + 3] = ok ? v.w : 0.0f;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EM; ++e) {
+      const bool ok = tok && e < E;
+      const float v = a.gates[ok ? lane * E + e : 0];
+      g[e] = ok ? v : 0.0f;
+    }
+  }
+  // with a budget of every expert, all are kept whatever the demand
+  unsigned long long keep = (1ull << E) - 1ull;
+  if (a.budget < E) keep = keep_set<EM>(a, g, tok, lane);
+  // masked top-2 of this lane's token
+  tmb::Top2 r{-1, -1, 0.0f, 0.0f};
+#pragma unroll
+  for (int e = 0; e < EM; ++e)
+    if (e < E) r.offer(((keep >> e) & 1ull) ? g[e] : 0.0f, e);
+  const int i1 = tok ? r.i1 : -1;
+  const int i2 = tok ? r.i2 : -1;
+  // per-expert counts, compact offsets and M-tiles on scalars
+  int cnt[EM], off_e[EM], ps[EM];
+  int run_off = 0, run_mt = 0;
+#pragma unroll
+  for (int e = 0; e < EM; ++e) {
+    cnt[e] = __popcll(__ballot(i1 == e || i2 == e));
+    off_e[e] = run_off;
+    ps[e] = run_mt;
+    run_off += cnt[e];
+    run_mt += (cnt[e] + C::PBM - 1) / C::PBM;
+  }
+  const int n_mt = min(run_mt, mt_max);
+  int mt, cb;
+  if (!job_of(l, n_mt, ncol, &mt, &cb)) return false;
+  int e = -1;
+#pragma unroll
+  for (int k = 0; k < EM; ++k)
+    if (e < 0 && mt < ps[k] + (cnt[k] + C::PBM - 1) / C::PBM) e = k;
+  if (e < 0) return false;
+  int cnt_e = 0, off_sel = 0, ps_sel = 0;
+#pragma unroll
+  for (int k = 0; k < EM; ++k)
+    if (k == e) {
+      cnt_e = cnt[k];
+      off_sel = off_e[k];
+      ps_sel = ps[k];
+    }
+  const int m0 = (mt - ps_sel) * C::PBM;
+  *e_out = e;
+  *m0_out = m0;
+  *p0_out = off_sel + m0;
+  *rows_out = min(C::PBM, cnt_e - m0);
+  *single_out = (cnt_e + C::PBM - 1) / C::PBM == 1;
+  *cb_out = cb;
+  *mask_out = __ballot(i1 == e || i2 == e);
+  return true;
+}
+
+template <class C, int DT, int EM>
+__global__ void __launch_bounds__(C::NT)
+tm_prefill_gemm1_routed_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w1,
+                               const uint16_t* __restrict__ w3, uint16_t* __restrict__ h,
+                               tmb::BucketArgs ra, int H, int I, int mt_max, uint32_t x_bytes) {
+  __shared__ __attribute__((aligned(16))) uint8_t s0[C::STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t s1[C::STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t s2[C::STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t s3[C::NSTAGE > 3 ? C::STAGE : 16];
+  static_assert(sizeof(RvShared) <= C::STAGE, "the routing writer uses the first stage");
+  const int L = (int)blockIdx.x;
+  if (L < kRvLeaders) {
+    if (L == 0) tmb::bucket_phases<C::NT, RvShared, true>(ra, *reinterpret_cast<RvShared*>(s0));
+    return;
+  }
+  int e, p0, rows, m0, cb;
+  bool single;
+  unsigned long long mask;
+  if (!rr_job<C, EM>(ra, L - kRvLeaders, I / (C::PBN / 2), mt_max, &e, &p0, &rows, &m0,
+                     &single, &cb, &mask))
+    return;
+  DmaLoad<C> d;
+  d.ra = pbuf(x, x_bytes);
+#pragma unroll
+  for (int i = 0; i < C::ALD; ++i) {
+    const int r = dma_row<C>(i);
+    d.aoff[i] = r < rows ? (uint32_t)nth_set_bit(mask, m0 + r) * (uint32_t)H * 2u +
+                               (uint32_t)dma_chunk<C>(r) * 16u
+                         : kOOR;
+  }
+  const Stages sb{s0, s1, s2, s3};
+  gemm1_job<C, DT>(sb, d, w1, w3, h, e, p0, rows, single, cb, H, I);
 }
 
 // ---------------------------------------------------------------- down --
@@ -584,6 +830,27 @@ int launch_gemm1(const void* x, const void* w1, const void* w3, void* h,
   return TM_OK;
 }
 
+// The self-routed gate/up launch with tile C.
+template <class C, int DT>
+int launch_gemm1_routed(const void* x, const void* w1, const void* w3, void* h,
+                        const tmb::BucketArgs& ra, int64_t T, int64_t H, int64_t I,
+                        hipStream_t stream) {
+  const int64_t mt_max = std::min<int64_t>(ra.max_tiles, mtile_bound<C>(2 * T, ra.E));
+  const int64_t jobs = launch_jobs(mt_max, I / (C::PBN / 2)) + kRvLeaders;
+  if (jobs > INT32_MAX) return TM_ERR_SHAPE;
+  if (ra.E <= 8)
+    hipLaunchKernelGGL((tm_prefill_gemm1_routed_kernel<C, DT, 8>), dim3((unsigned)jobs),
+                       dim3(C::NT), 0, stream, (const uint16_t*)x, (const uint16_t*)w1,
+                       (const uint16_t*)w3, (uint16_t*)h, ra, (int)H, (int)I, (int)mt_max,
+                       (uint32_t)(T * H * 2));
+  else
+    hipLaunchKernelGGL((tm_prefill_gemm1_routed_kernel<C, DT, kRrMaxExperts>),
+                       dim3((unsigned)jobs), dim3(C::NT), 0, stream, (const uint16_t*)x,
+                       (const uint16_t*)w1, (const uint16_t*)w3, (uint16_t*)h, ra, (int)H,
+                       (int)I, (int)mt_max, (uint32_t)(T * H * 2));
+  return TM_OK;
+}
+
 }  // namespace
 
 extern "C" int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w3, void* h,
@@ -626,6 +893,64 @@ extern "C" int tm_op1_prefill_gemm1(const void* x, const void* w1, const void* w
                                                    tiles, max_tiles, T, H, I, E, st)
              : launch_gemm1<Tile128, TM_DTYPE_BF16>(x, w1, w3, h, sorted_slots, expert_offsets,
                                                     tiles, max_tiles, T, H, I, E, st);
+  }
+  if (rc) return rc;
+  TM_HIP_CHECK_LAUNCH();
+  return TM_OK;
+}
+
+extern "C" int tm_op1_prefill_gemm1_routed(
+    const void* x, const void* w1, const void* w3, void* h, const float* gates,
+    const float* accept, int64_t T, int64_t H, int64_t I, int64_t E, int64_t budget, float tau,
+    int objective, int64_t block_m, int64_t max_blocks, int64_t max_tiles, int64_t* topk_ids,
+    float* gates_flat, int64_t* padded_slots, int64_t* block_expert_ids, int64_t* slot_to_row,
+    float* demand, int32_t* expert_offsets, int32_t* sorted_slots, int32_t* slot_pos,
+    int32_t* tiles, int dtype, void* stream) {
+  if (T < 1 || T > kRrMaxTokens || E < 2 || E > kRrMaxExperts) return TM_ERR_SHAPE;
+  if (budget < 2 || budget > E) return TM_ERR_ARG;
+  if (objective != TM_OBJECTIVE_MASS && objective != TM_OBJECTIVE_CRITICAL_PATH) return TM_ERR_ARG;
+  if (block_m != 16 && block_m != 32) return TM_ERR_ARG;
+  if (max_blocks < 1 || max_blocks > kRvMaxBlocks || max_tiles < 1) return TM_ERR_SHAPE;
+  if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
+  if (H < Tile128::PBK || (H % Tile128::PBK) != 0 || I < Tile128::PBN / 2 ||
+      (I % (Tile128::PBN / 2)) != 0)
+    return TM_ERR_SHAPE;
+  if (I * H * 2 >= (int64_t)kOOR || T * H * 2 >= (int64_t)kOOR || 2 * T * I * 2 >= (int64_t)kOOR)
+    return TM_ERR_SHAPE;
+  if (!aligned16(x) || !aligned16(w1) || !aligned16(w3) || !aligned16(h)) return TM_ERR_ALIGN;
+  tmb::BucketArgs ra;
+  ra.gates = gates;
+  ra.accept = accept;
+  ra.T = (int)T;
+  ra.E = (int)E;
+  ra.budget = (int)budget;
+  ra.objective = objective;
+  ra.BM = (int)block_m;
+  ra.max_blocks = (int)max_blocks;
+  ra.max_tiles = (int)max_tiles;
+  ra.tau = tau;
+  ra.topk_ids = topk_ids;
+  ra.gates_flat = gates_flat;
+  ra.padded_slots = padded_slots;
+  ra.block_expert_ids = block_expert_ids;
+  ra.slot_to_row = slot_to_row;
+  ra.demand_out = demand;
+  ra.expert_offsets = expert_offsets;
+  ra.sorted_slots = sorted_slots;
+  ra.slot_pos = slot_pos;
+  ra.tiles = tiles;
+  // the tile rule of tm_op1_prefill_gemm1 (2T < 384 E here, so never the
+  // 256-row tile)
+  const bool dec = 2 * T <= 16 * max_tiles;
+  const hipStream_t st = (hipStream_t)stream;
+  const bool f16 = dtype == TM_DTYPE_F16;
+  int rc;
+  if (dec) {
+    rc = f16 ? launch_gemm1_routed<TileDec, TM_DTYPE_F16>(x, w1, w3, h, ra, T, H, I, st)
+             : launch_gemm1_routed<TileDec, TM_DTYPE_BF16>(x, w1, w3, h, ra, T, H, I, st);
+  } else {
+    rc = f16 ? launch_gemm1_routed<Tile128, TM_DTYPE_F16>(x, w1, w3, h, ra, T, H, I, st)
+             : launch_gemm1_routed<Tile128, TM_DTYPE_BF16>(x, w1, w3, h, ra, T, H, I, st);
   }
   if (rc) return rc;
   TM_HIP_CHECK_LAUNCH();

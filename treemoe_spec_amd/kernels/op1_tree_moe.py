@@ -6,7 +6,10 @@ Same Python surface as the reference module treemoe/kernels/op1_tree_moe.py
 work runs in libtreemoe_amd.so:
 
   routing      tm_op1_route          router (bf16 logits, fp32 softmax), then
-                                     budget routing + bucketing (two launches)
+                                     budget routing + bucketing (two launches);
+                                     at few tokens on the tiled path the
+                                     bucketing runs inside the gate/up launch
+                                     (tm_op1_prefill_gemm1_routed)
   gate/up      tm_op1_gemm1          MFMA, SwiGLU fused, h kept in bf16
   down         tm_op1_gemm2          MFMA, deterministic K split, gate applied
   combine      tm_op1_combine        fixed order, bf16 output
@@ -351,6 +354,22 @@ class Routing:
         return picked
 
 
+def _routing_of(ws: _Workspace, n: int, expert_budget: int) -> Routing:
+    """The Routing handle over the workspace's routing buffers."""
+    max_blocks = compact_block_capacity(2 * n, expert_budget, BM)
+    launch_blocks = compact_block_limit(2 * n, expert_budget, BM)
+    max_tiles = compact_block_limit(2 * n, expert_budget, TILE_M)
+    return Routing(ws, ws.router_gates, ws.topk_flat.view(n, 2), ws.gates_flat,
+                   ws.padded_slots[: max_blocks * BM], ws.block_expert_ids[:max_blocks],
+                   ws.slot_to_row, max_blocks, launch_blocks, ws.demand, ws.expert_offsets,
+                   ws.sorted_slots, ws.slot_pos, ws.tiles[:max_tiles], max_tiles)
+
+
+def _check_router(x: torch.Tensor, router_weight: torch.Tensor) -> None:
+    if router_weight.shape[1] != x.shape[1]:
+        raise ValueError("router_weight must be [E, H] with H = x.shape[1]")
+
+
 def route_experts(
     x: torch.Tensor,
     router_weight: torch.Tensor,
@@ -367,25 +386,37 @@ def route_experts(
     _require_device(x, router_weight, node_accept_prob)
     _require_half("x", x)
     _require_half("router_weight", router_weight, like=x)
+    _check_router(x, router_weight)
     n, hidden = x.shape
     e = router_weight.shape[0]
-    if router_weight.shape[1] != hidden:
-        raise ValueError("router_weight must be [E, H] with H = x.shape[1]")
     ws = _workspace(n, e, hidden, inter, x)
     accept = _prep_accept(node_accept_prob, n)
-    max_blocks = compact_block_capacity(2 * n, expert_budget, BM)
-    launch_blocks = compact_block_limit(2 * n, expert_budget, BM)
-    max_tiles = compact_block_limit(2 * n, expert_budget, TILE_M)
-    padded = ws.padded_slots[: max_blocks * BM]
-    blk = ws.block_expert_ids[:max_blocks]
-    tiles = ws.tiles[:max_tiles]
+    r = _routing_of(ws, n, expert_budget)
     _launch_route(x, router_weight, accept, expert_budget, top1_threshold, routing_objective,
-                  BM, max_blocks, max_tiles, ws.router_gates, ws.topk_flat, ws.gates_flat,
-                  padded, blk, ws.slot_to_row, ws.demand, ws.expert_offsets, ws.sorted_slots,
-                  ws.slot_pos, tiles)
-    return Routing(ws, ws.router_gates, ws.topk_flat.view(n, 2), ws.gates_flat, padded, blk,
-                   ws.slot_to_row, max_blocks, launch_blocks, ws.demand, ws.expert_offsets,
-                   ws.sorted_slots, ws.slot_pos, tiles, max_tiles)
+                  BM, r.max_blocks, r.max_tiles, ws.router_gates, ws.topk_flat, ws.gates_flat,
+                  r.padded_slots, r.block_expert_ids, ws.slot_to_row, ws.demand,
+                  ws.expert_offsets, ws.sorted_slots, ws.slot_pos, r.tiles)
+    return r
+
+
+# At few tokens the tiled gate/up launch routes its own jobs and writes the
+# routing outputs itself (tm_op1_prefill_gemm1_routed): the budget routing and
+# bucketing launch and its launch gap leave the layer's critical path.  Limits
+# of that entry point (one token per lane of a wave, a token's gates in
+# registers):
+SELF_ROUTED_MAX_TOKENS = 64
+SELF_ROUTED_MAX_EXPERTS = 16
+_SELF_ROUTED_MAX_BLOCKS = 256      # compact_block_capacity(2T, B, BM)
+
+
+def self_routed(num_tokens: int, expert_budget: int, num_experts: int, inter: int) -> bool:
+    """True when tree_moe_forward (without a precomputed routing) runs the
+    routing inside the gate/up launch: the tiled GEMMs at few tokens."""
+    return (uses_tiled_gemms(num_tokens, expert_budget, num_experts, inter)
+            and num_tokens <= SELF_ROUTED_MAX_TOKENS
+            and num_experts <= SELF_ROUTED_MAX_EXPERTS
+            and compact_block_capacity(2 * num_tokens, expert_budget, BM)
+            <= _SELF_ROUTED_MAX_BLOCKS)
 
 
 def tree_moe_forward(
@@ -407,6 +438,15 @@ def tree_moe_forward(
     and the combine sums them in a fixed order, so ``deterministic=False``
     (the reference's atomic variant) returns the same bits.  ``routing`` is a
     precomputed phase-1 handle from route_experts(); None routes inline."""
+    return _forward(x, w1, w2, w3, router_weight, node_accept_prob, expert_budget, out,
+                    routing, routing_objective)
+
+
+def _forward(x, w1, w2, w3, router_weight, node_accept_prob, expert_budget, out, routing,
+             routing_objective, on_phase=None) -> torch.Tensor:
+    """tree_moe_forward's launches.  ``on_phase(name)``, when given, is called
+    after the launches of each phase ("route", "gemm1", "gemm2", "combine"):
+    the benchmark records its events there."""
     _check_budget(expert_budget, router_weight.shape[0], routing_objective)
     _require_device(x, w1, w2, w3, router_weight, node_accept_prob)
     dt = _require_half("x", x)
@@ -418,9 +458,32 @@ def tree_moe_forward(
         raise ValueError("expected w1, w3 [E, I, H] and w2 [E, H, I] matching x [T, H]")
     if hidden % 256 != 0 or inter % 256 != 0:
         raise ValueError("hidden and intermediate sizes must be multiples of 256")
-    if routing is None:
-        routing = route_experts(x, router_weight, node_accept_prob, expert_budget, inter,
-                                routing_objective=routing_objective)
+    tiled = uses_tiled_gemms(n, expert_budget, e, inter)
+    if routing is None and self_routed(n, expert_budget, e, inter):
+        # router, then the gate/up launch that also routes and buckets
+        _check_router(x, router_weight)
+        stream = _capi.stream_of(x.device)
+        ws = _workspace(n, e, hidden, inter, x)
+        accept = _prep_accept(node_accept_prob, n)
+        routing = _routing_of(ws, n, expert_budget)
+        _launch_router(x, router_weight, ws.router_gates)
+        if on_phase is not None:
+            on_phase("route")
+        call("tm_op1_prefill_gemm1_routed", ptr(x), ptr(w1), ptr(w3), ptr(ws.h),
+             ptr(ws.router_gates), ptr(accept), n, hidden, inter, e, expert_budget, 0.05,
+             TM_OBJECTIVE[routing_objective], BM, routing.max_blocks, routing.max_tiles,
+             ptr(ws.topk_flat), ptr(ws.gates_flat), ptr(routing.padded_slots),
+             ptr(routing.block_expert_ids), ptr(ws.slot_to_row), ptr(ws.demand),
+             ptr(ws.expert_offsets), ptr(ws.sorted_slots), ptr(ws.slot_pos),
+             ptr(routing.tiles), dt, stream)
+        gemm1_done = True
+    else:
+        if routing is None:
+            routing = route_experts(x, router_weight, node_accept_prob, expert_budget, inter,
+                                    routing_objective=routing_objective)
+        if on_phase is not None:
+            on_phase("route")
+        gemm1_done = False
     ws = routing.ws
     if (routing.topk_ids.shape[0] != n or ws.partial.shape[1] != 2 * n
             or ws.h.shape != (ws.max_tiles * TILE_M, inter) or ws.partial.shape[2] != hidden
@@ -429,20 +492,27 @@ def tree_moe_forward(
         raise ValueError("routing was computed for a different shape")
     stream = _capi.stream_of(x.device)
     split = ws.split
-    if uses_tiled_gemms(n, expert_budget, e, inter):
+    if tiled:
         split = _tiled_split(n, expert_budget, e, hidden, inter, ws)
-        call("tm_op1_prefill_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h),
-             ptr(routing.sorted_slots), ptr(routing.expert_offsets), ptr(routing.tiles),
-             routing.max_tiles, n, hidden, inter, e, dt, stream)
+        if not gemm1_done:
+            call("tm_op1_prefill_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h),
+                 ptr(routing.sorted_slots), ptr(routing.expert_offsets), ptr(routing.tiles),
+                 routing.max_tiles, n, hidden, inter, e, dt, stream)
+        if on_phase is not None:
+            on_phase("gemm1")
         call("tm_op1_prefill_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial),
              ptr(routing.gates_flat), ptr(routing.sorted_slots), ptr(routing.expert_offsets),
              ptr(routing.tiles), routing.max_tiles, split, n, hidden, inter, e, dt, stream)
     else:
         call("tm_op1_gemm1", ptr(x), ptr(w1), ptr(w3), ptr(ws.h), ptr(routing.sorted_slots),
              ptr(routing.tiles), routing.max_tiles, n, hidden, inter, e, dt, stream)
+        if on_phase is not None:
+            on_phase("gemm1")
         call("tm_op1_gemm2", ptr(ws.h), ptr(w2), ptr(ws.partial), ptr(routing.gates_flat),
              ptr(routing.sorted_slots), ptr(routing.tiles), routing.max_tiles, ws.split, n,
              hidden, inter, e, dt, stream)
+    if on_phase is not None:
+        on_phase("gemm2")
     if out is not None:
         if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
             raise ValueError("out must be a contiguous tensor like x")
@@ -451,4 +521,6 @@ def tree_moe_forward(
         result = torch.empty_like(x)
     call("tm_op1_combine", ptr(ws.partial), ptr(routing.slot_pos), ptr(result), n, hidden,
          split, dt, stream)
+    if on_phase is not None:
+        on_phase("combine")
     return result
