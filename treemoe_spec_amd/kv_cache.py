@@ -63,35 +63,54 @@ class PagedKVCache:
         self._dev_table_len = -1
         self._dev_scratch: torch.Tensor | None = None
 
+    # Positions map to flat slots of the [pages * page_size] axis:
+    # slot = block_table[q // page_size] * page_size + q % page_size.  The
+    # host-side paths below (prefill append, the reference's gather for SDPA,
+    # the host commit) all go through that map and index_select / index_copy_
+    # on the flat view, one op per tensor.
+
     def reset(self) -> None:
-        """Start a new sequence without clearing the backing tensors."""
-        self._free.extend(reversed(self.block_table))
-        self.block_table.clear()
+        """Start a new sequence; the backing tensors keep their contents and
+        the sequence's pages return to the free list."""
+        while self.block_table:
+            self._free.append(self.block_table.pop())
         self.seq_len = 0
         self._dev_table_len = -1
 
     def _ensure_capacity(self, new_len: int) -> None:
-        while len(self.block_table) * self.block_size < new_len:
-            if not self._free:
-                raise RuntimeError("KV cache out of blocks")
+        """Map enough pages for positions 0 .. new_len - 1."""
+        missing = -(-new_len // self.block_size) - len(self.block_table)
+        if missing <= 0:
+            return
+        if missing > len(self._free):
+            raise RuntimeError("KV cache out of blocks")
+        for _ in range(missing):
             self.block_table.append(self._free.pop())
 
     def slot_of(self, pos: int) -> tuple[int, int]:
-        return self.block_table[pos // self.block_size], pos % self.block_size
+        page, off = divmod(pos, self.block_size)
+        return self.block_table[page], off
+
+    def _flat_slots(self, start: int, count: int) -> torch.Tensor:
+        """Flat slots of positions start .. start + count - 1 (mapped pages)."""
+        dev = self.k.device
+        pos = torch.arange(start, start + count, device=dev, dtype=torch.long)
+        table = torch.tensor(self.block_table, device=dev, dtype=torch.long)
+        return table[pos // self.block_size] * self.block_size + pos % self.block_size
+
+    def _flat(self, t: torch.Tensor, layer: int) -> torch.Tensor:
+        """[pages * page_size, kv_heads, head_dim] view of one layer."""
+        return t[layer].flatten(0, 1)
 
     def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, start_pos: int) -> None:
         """Write [T, kv_heads, head_dim] at positions start_pos .. start_pos+T-1
-        (prefill and autoregressive steps; reference kv_cache.py:62-78).  Page
-        and offset indices are computed on the host from block_table."""
+        (prefill and autoregressive steps; the contract of the reference's
+        append, kv_cache.py:62-78)."""
         t = k.shape[0]
         self._ensure_capacity(start_pos + t)
-        bs = self.block_size
-        pos = range(start_pos, start_pos + t)
-        blks = torch.tensor([self.block_table[q // bs] for q in pos], device=self.k.device,
-                            dtype=torch.long)
-        offs = torch.tensor([q % bs for q in pos], device=self.k.device, dtype=torch.long)
-        self.k[layer, blks, offs] = k
-        self.v[layer, blks, offs] = v
+        slots = self._flat_slots(start_pos, t)
+        self._flat(self.k, layer).index_copy_(0, slots, k.to(self.k.dtype))
+        self._flat(self.v, layer).index_copy_(0, slots, v.to(self.v.dtype))
         self.seq_len = max(self.seq_len, start_pos + t)
 
     def write_tree(self, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
@@ -122,12 +141,11 @@ class PagedKVCache:
         dev = self.k.device
         slots = valid.to(device=dev, dtype=torch.long)
         pages = torch.tensor(self.tree_pages, device=dev, dtype=torch.long)
-        src_p, src_o = pages[slots // bs], slots % bs
-        dest = [self.slot_of(self.seq_len + j) for j in range(m)]
-        dst_p = torch.tensor([d[0] for d in dest], device=dev, dtype=torch.long)
-        dst_o = torch.tensor([d[1] for d in dest], device=dev, dtype=torch.long)
-        self.k[:, dst_p, dst_o] = self.k[:, src_p, src_o]
-        self.v[:, dst_p, dst_o] = self.v[:, src_p, src_o]
+        src = pages[slots // bs] * bs + slots % bs
+        dst = self._flat_slots(self.seq_len, m)
+        for cache in (self.k, self.v):
+            flat = cache.flatten(1, 2)  # [layers, pages * page_size, kv_heads, head_dim]
+            flat[:, dst] = flat[:, src]
         self.seq_len += m
 
     def device_tables(self, device) -> tuple[torch.Tensor, torch.Tensor]:
@@ -146,37 +164,30 @@ class PagedKVCache:
         return self._dev_table, self._dev_scratch
 
     def gather(self, layer: int, upto: int | None = None):
-        """Contiguous [T, kv_heads, head_dim] K and V of positions 0..T-1."""
+        """Contiguous [T, kv_heads, head_dim] K and V of positions 0..T-1
+        (the reference's gather, kv_cache.py:110-123)."""
         t = self.seq_len if upto is None else upto
-        nblk = (t + self.block_size - 1) // self.block_size
-        idx = torch.tensor(self.block_table[:nblk], device=self.k.device, dtype=torch.long)
-        kvh, hd = self.k.shape[3], self.k.shape[4]
-        k = self.k[layer, idx].reshape(nblk * self.block_size, kvh, hd)[:t]
-        v = self.v[layer, idx].reshape(nblk * self.block_size, kvh, hd)[:t]
-        return k, v
+        slots = self._flat_slots(0, t)
+        return (self._flat(self.k, layer).index_select(0, slots),
+                self._flat(self.v, layer).index_select(0, slots))
 
     def gather_with_tail(self, layer: int, k_tail: torch.Tensor,
                          v_tail: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """Contiguous [seq_len + T, kv_heads, head_dim] K and V: the committed
-        prefix followed by the tree rows (reference kv_cache.py:125-145, the
-        input of the reference's SDPA tree attention; this build's tree
-        attention reads the pages in place instead)."""
+        prefix followed by the tree rows, each written once into the result
+        (the contract of the reference's gather_with_tail, kv_cache.py:125-145,
+        the input of its SDPA tree attention; this build's tree attention
+        reads the pages in place instead)."""
         s, t = self.seq_len, k_tail.shape[0]
-        bs = self.block_size
-        nblk = (s + bs - 1) // bs
-        idx = torch.tensor(self.block_table[:nblk], device=self.k.device, dtype=torch.long)
-        kvh, hd = self.k.shape[3], self.k.shape[4]
-        m = max(nblk * bs, s + t)
-        out_k = torch.empty(m, kvh, hd, device=self.k.device, dtype=self.k.dtype)
-        out_v = torch.empty_like(out_k)
-        if nblk:
-            torch.index_select(self.k[layer], 0, idx,
-                               out=out_k[:nblk * bs].view(nblk, bs, kvh, hd))
-            torch.index_select(self.v[layer], 0, idx,
-                               out=out_v[:nblk * bs].view(nblk, bs, kvh, hd))
-        out_k[s:s + t] = k_tail
-        out_v[s:s + t] = v_tail
-        return out_k[:s + t], out_v[:s + t]
+        slots = self._flat_slots(0, s)
+        out = []
+        for cache, tail in ((self.k, k_tail), (self.v, v_tail)):
+            buf = torch.empty((s + t,) + tuple(cache.shape[3:]), device=cache.device,
+                              dtype=cache.dtype)
+            torch.index_select(self._flat(cache, layer), 0, slots, out=buf[:s])
+            buf[s:] = tail
+            out.append(buf)
+        return out[0], out[1]
 
 
 def scratch_pages_of(kv) -> list[int]:
