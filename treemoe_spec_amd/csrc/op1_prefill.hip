@@ -36,7 +36,9 @@
 // M-tiles are BM consecutive rows of one expert in the compact expert-major
 // order (expert_offsets).  Launch order: workgroups are dealt to the 8 XCDs
 // in turn, and each XCD owns one eighth of the column jobs for every M-tile,
-// walked in super-blocks of 8 M-tiles x 4 columns (job_of).
+// walked expert by expert, M fastest, when the experts average two M-tiles
+// or more, else in super-blocks of 8 M-tiles x 4 columns (expert_job; the
+// self-routed decode gate/up always takes the super-blocks, job_of).
 #pragma clang fp contract(off)
 
 #include <algorithm>
@@ -129,26 +131,9 @@ constexpr int kXcds = 8;  // workgroup i runs on XCD i % 8
 constexpr int SBM = 8;    // super-block: M-tile slots (consecutive: mostly one expert) ..
 constexpr int SBN = 4;    // .. x column jobs, M fastest
 
-// Real M-tiles of this layer: sum over experts of ceil(rows_e / BM), from the
-// compact offsets (computed by every workgroup; E <= 64 loads).
-template <class C>
-__device__ __forceinline__ int count_mtiles(const int32_t* __restrict__ offsets, int E) {
-  __shared__ int s_n;
-  if (threadIdx.x < 64) {
-    int n = 0;
-    if ((int)threadIdx.x < E) {
-      const int cnt = offsets[threadIdx.x + 1] - offsets[threadIdx.x];
-      n = (cnt + C::PBM - 1) / C::PBM;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) n += __shfl_xor(n, o);
-    if (threadIdx.x == 0) s_n = n;
-  }
-  __syncthreads();
-  return s_n;
-}
-
-// Job of launch index L over the layer's real M-tiles (n_mt of them): M-tile
+// Job of launch index L over the layer's real M-tiles (n_mt of them) in the
+// super-block order (the self-routed decode gate/up, whose waves compute it
+// in registers, and expert_job when most experts take one M-tile): M-tile
 // and column job, or false for a launch index past the real jobs (those are
 // the launch's last indices, so the real jobs all start in the first round).
 // XCD x = L % 8 owns the column jobs [x * cpx, (x + 1) * cpx) for every
@@ -170,6 +155,68 @@ __device__ __forceinline__ bool job_of(int L, int n_mt, int ncol, int* mt, int* 
   *mt = g * SBM + jj % mg;
   *col = x * cpx + s * SBN + jj / mg;
   return *col < ncol;
+}
+
+// Job of launch index L for the prefill GEMMs: M-tile (in the compact
+// expert-major order) and column job, or false for a launch index past the
+// real jobs (those are the launch's last indices).  The first wave scans
+// ceil(rows_e / BM) over the experts (E <= 64 loads).  When the active
+// experts average two M-tiles or more, XCD x = L % 8 walks its column jobs
+// [x * cpx, (x + 1) * cpx) of every M-tile one expert at a time, the
+// expert's M-tiles fastest, then its columns: the ~32 workgroups resident on
+// an XCD then run the jobs of one expert or of a few adjacent ones, so all
+// the M-tiles that read a weight block run together and share it in that
+// L2, and each A tile is shared by the expert's nearby columns.  With fewer
+// M-tiles it takes the super-block order (job_of), whose resident jobs read
+// several experts' weights at once.  (Same box, bit-identical, expert order
+// against super-blocks: config 5 1787 against 1801 us, T = 2048 uniform 1719
+// against 1771, T = 4096 3111 against 3202, T = 1536 1374 against 1411; but
+// T = 128 535 against 501, T = 256 542 against 513, T = 512 720 against 705,
+// where most experts take one M-tile.)
+template <class C>
+__device__ __forceinline__ bool expert_job(int L, const int32_t* __restrict__ offsets, int E,
+                                           int mt_max, int ncol, int* mt, int* col) {
+  __shared__ int s_mt, s_col;
+  const int x = L % kXcds, l = L / kXcds;
+  const int cpx = (ncol + kXcds - 1) / kXcds;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    int n = 0;
+    if (lane < E) {
+      const int cnt = offsets[lane + 1] - offsets[lane];
+      n = (cnt + C::PBM - 1) / C::PBM;
+    }
+    int incl = n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
+    }
+    const int first = incl - n;  // M-tiles of the experts before this lane's
+    const int total = __shfl(incl, 63);
+    const int active = __popcll(__ballot(n > 0));
+    if (total < 2 * active) {
+      // Mostly one M-tile per expert: the super-block order, whose jobs
+      // resident together read different experts' weights.
+      if (lane == 0) {
+        int mt = -1, col = 0;
+        const bool ok = job_of(L, min(total, mt_max), ncol, &mt, &col);
+        s_mt = ok ? mt : -1;
+        s_col = col;
+      }
+    } else {
+      if (lane == 0) s_mt = -1;  // (LDS stores of one wave land in order)
+      if (n > 0 && l >= first * cpx && l < incl * cpx) {
+        const int j = l - first * cpx;
+        s_mt = first + j % n;
+        s_col = x * cpx + j / n;
+      }
+    }
+  }
+  __syncthreads();
+  *mt = s_mt;
+  *col = s_col;
+  return *mt >= 0 && *mt < mt_max && *col < ncol;
 }
 
 // Launch size: 8 XCDs x (M-tile bound) x the columns of one XCD's range.
@@ -460,8 +507,7 @@ tm_prefill_gemm1_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
   const Stages sb{s0, s1, s2, s3};
   int mt, cb;
   const int ncol = I / (C::PBN / 2);
-  const int n_mt = min(count_mtiles<C>(offsets, E), mt_max);
-  if (!job_of((int)blockIdx.x, n_mt, ncol, &mt, &cb)) return;
+  if (!expert_job<C>((int)blockIdx.x, offsets, E, mt_max, ncol, &mt, &cb)) return;
   int e, p0, rows;
   bool single;
   if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows, &single)) return;
@@ -765,8 +811,7 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   static_assert(C::NW == 8, "down GEMM: 8 waves, 64 output columns per column group");
   int mt, job;  // job = (column block, segment)
   const int ncol = (H / C::PBN) * nsplit;
-  const int n_mt = min(count_mtiles<C>(offsets, E), mt_max);
-  if (!job_of((int)blockIdx.x, n_mt, ncol, &mt, &job)) return;
+  if (!expert_job<C>((int)blockIdx.x, offsets, E, mt_max, ncol, &mt, &job)) return;
   const int cb = job / nsplit;
   const int seg = job - cb * nsplit;
   int e, p0, rows;
