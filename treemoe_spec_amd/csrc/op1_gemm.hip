@@ -398,8 +398,11 @@ static_assert(kScratchBytes >= WAVES * 4 * 2 * 64 * 16, "gemm1 reduction");
 
 // --------------------------------------------------------------- combine --
 // out[t, n] = bf16( sum over (k = 0, 1) of sum over split s of y[s, pos(2t+k), n] ),
-// accumulated in exactly that order from 0.
-template <int DT>
+// accumulated in exactly that order from 0.  SC > 0 is the split count known
+// at compile time: all 2 SC loads are issued before the first add, so the
+// thread waits for one memory round trip instead of one per partial (with a
+// run-time count the loop waits for each load before the next is issued).
+template <int DT, int SC>
 __global__ void __launch_bounds__(256)
 tm_combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ slot_pos,
                   uint16_t* __restrict__ out, int T, int H, int S, int R) {
@@ -409,13 +412,26 @@ tm_combine_kernel(const float* __restrict__ y, const int32_t* __restrict__ slot_
   const int p0 = slot_pos[2 * t];
   const int p1 = slot_pos[2 * t + 1];
   float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  for (int s = 0; s < S; ++s) {
-    const float4 v = *reinterpret_cast<const float4*>(y + ((size_t)s * R + p0) * H + n);
-    a0 = a0 + v.x; a1 = a1 + v.y; a2 = a2 + v.z; a3 = a3 + v.w;
-  }
-  for (int s = 0; s < S; ++s) {
-    const float4 v = *reinterpret_cast<const float4*>(y + ((size_t)s * R + p1) * H + n);
-    a0 = a0 + v.x; a1 = a1 + v.y; a2 = a2 + v.z; a3 = a3 + v.w;
+  if constexpr (SC > 0) {
+    float4 v[2 * SC];
+#pragma unroll
+    for (int s = 0; s < SC; ++s) {
+      v[s] = *reinterpret_cast<const float4*>(y + ((size_t)s * R + p0) * H + n);
+      v[SC + s] = *reinterpret_cast<const float4*>(y + ((size_t)s * R + p1) * H + n);
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * SC; ++i) {
+      a0 = a0 + v[i].x; a1 = a1 + v[i].y; a2 = a2 + v[i].z; a3 = a3 + v[i].w;
+    }
+  } else {
+    for (int s = 0; s < S; ++s) {
+      const float4 v = *reinterpret_cast<const float4*>(y + ((size_t)s * R + p0) * H + n);
+      a0 = a0 + v.x; a1 = a1 + v.y; a2 = a2 + v.z; a3 = a3 + v.w;
+    }
+    for (int s = 0; s < S; ++s) {
+      const float4 v = *reinterpret_cast<const float4*>(y + ((size_t)s * R + p1) * H + n);
+      a0 = a0 + v.x; a1 = a1 + v.y; a2 = a2 + v.z; a3 = a3 + v.w;
+    }
   }
   u16x4_t o;
   o[0] = Half16<DT>::round(a0);
@@ -485,9 +501,15 @@ extern "C" int tm_op1_combine(const float* y, const int32_t* slot_pos, void* out
   if (dtype != TM_DTYPE_BF16 && dtype != TM_DTYPE_F16) return TM_ERR_ARG;
   if (!aligned16(y) || ((uintptr_t)out % 8) != 0) return TM_ERR_ALIGN;
   const dim3 grid((unsigned)T, (unsigned)((H + 1023) / 1024));
-  hipLaunchKernelGGL(dtype == TM_DTYPE_F16 ? tm_combine_kernel<TM_DTYPE_F16>
-                                           : tm_combine_kernel<TM_DTYPE_BF16>,
-                     grid, dim3(256), 0, (hipStream_t)stream, y, slot_pos,
+  const bool f16 = dtype == TM_DTYPE_F16;
+  void (*kern)(const float*, const int32_t*, uint16_t*, int, int, int, int);
+  switch (split) {  // the split counts the forward uses
+    case 1: kern = f16 ? tm_combine_kernel<TM_DTYPE_F16, 1> : tm_combine_kernel<TM_DTYPE_BF16, 1>; break;
+    case 2: kern = f16 ? tm_combine_kernel<TM_DTYPE_F16, 2> : tm_combine_kernel<TM_DTYPE_BF16, 2>; break;
+    case 4: kern = f16 ? tm_combine_kernel<TM_DTYPE_F16, 4> : tm_combine_kernel<TM_DTYPE_BF16, 4>; break;
+    default: kern = f16 ? tm_combine_kernel<TM_DTYPE_F16, 0> : tm_combine_kernel<TM_DTYPE_BF16, 0>;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, (hipStream_t)stream, y, slot_pos,
                      (uint16_t*)out, (int)T, (int)H, (int)split, (int)(2 * T));
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
