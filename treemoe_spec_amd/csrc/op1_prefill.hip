@@ -563,14 +563,13 @@ __device__ __forceinline__ int nth_set_bit(unsigned long long m, int j) {
 }
 
 // The kept experts (bit e) from the demand and criticality of every token
-// held in its lane (g: the lane's gates, zero past E or T), as the phases
-// compute them.
+// held in its lane (g: the lane's gates, zero past E or T; a_ld: the lane's
+// accept probability, loaded with the gates), as the phases compute them.
 template <int EM>
 __device__ __forceinline__ unsigned long long keep_set(const tmb::BucketArgs& a,
-                                                       const float (&g)[EM], bool tok,
-                                                       int lane) {
+                                                       const float (&g)[EM], float a_ld,
+                                                       bool tok, int lane) {
   const int E = a.E;
-  const float a_ld = a.accept[tok ? lane : 0];
   const float av = tok ? a_ld : 0.0f;
   const bool critical = a.objective == TM_OBJECTIVE_CRITICAL_PATH;
   // demand: the EM halving trees, level by level
@@ -657,6 +656,9 @@ __device__ __forceinline__ bool rr_job(const tmb::BucketArgs& a, int l, int ncol
   const int lane = threadIdx.x & 63;
   const int T = a.T, E = a.E;
   const bool tok = lane < T;
+  // the accept probability is read with the gates (one memory round trip:
+  // loaded after the gates had arrived it cost a second one, ~2 us per job)
+  const float a_ld = a.accept[tok ? lane : 0];
   float g[EM];
   if ((E & 3) == 0 && (reinterpret_cast<uintptr_t>(a.gates) & 15) == 0) {
 #pragma unroll
@@ -678,7 +680,7 @@ __device__ __forceinline__ bool rr_job(const tmb::BucketArgs& a, int l, int ncol
   }
   // with a budget of every expert, all are kept whatever the demand
   unsigned long long keep = (1ull << E) - 1ull;
-  if (a.budget < E) keep = keep_set<EM>(a, g, tok, lane);
+  if (a.budget < E) keep = keep_set<EM>(a, g, a_ld, tok, lane);
   // masked top-2 of this lane's token
   tmb::Top2 r{-1, -1, 0.0f, 0.0f};
 #pragma unroll
