@@ -497,14 +497,14 @@ def secondary(m, inp2, args) -> dict:
     g = torch.Generator().manual_seed(5)
     q = torch.softmax(torch.randn(n, v, generator=g), -1).cuda()
     uni = torch.rand(n, generator=g).cuda()
-    bu = torch.rand(1, generator=g).cuda()
+    bonus_exp = torch.empty(v).exponential_(1.0, generator=g).cuda()
     resid = torch.empty(v, dtype=torch.float32, device=dev)
 
     def sample_step():
         _capi.call("tm_op4_sample_walk", logits.data_ptr(), _capi.TM_DTYPE_BF16, n, v,
                    logits.stride(0), q.data_ptr(), q.stride(0), tokens.data_ptr(), csr.data_ptr(),
                    csr.data_ptr() + 4 * n, csr.data_ptr() + 8 * n, num_edges, uni.data_ptr(),
-                   bu.data_ptr(),
+                   bonus_exp.data_ptr(),
                    1.0, resid.data_ptr(), slots.data_ptr(), toks.data_ptr(), result.data_ptr(),
                    stream)
 

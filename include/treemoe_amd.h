@@ -49,12 +49,13 @@ extern "C" {
 #define TM_OP4_MAX_PARTS 64    /* row ranges per node in the argmax workspace  */
 #define TM_OP4_NOALLOC_MAX_NODES 2048  /* N limit of tm_op4_argmax_walk_noalloc */
 
-/* ABI version (major*10000 + minor*100 + patch): 4.1.0.  Version 2 added
+/* ABI version (major*10000 + minor*100 + patch): 5.0.0.  Version 2 added
  * num_edges to tm_op4_argmax_walk / tm_op4_sample_walk and softmax_argmax to
  * tm_op4_argmax_walk; version 3 added host_count to tm_op4_kv_commit;
  * version 4 added `dtype` (TM_DTYPE_BF16 or TM_DTYPE_F16) to the op1 entry
  * points that read or write 16-bit activations or weights; 4.1 added
- * tm_op1_prefill_gemm1_routed. */
+ * tm_op1_prefill_gemm1_routed; version 5 made tm_op4_sample_walk's bonus
+ * argument V exponential draws (bonus_exp) instead of one uniform. */
 int tm_version(void);
 
 /* Human-readable text for a return code of any entry point. */
@@ -310,18 +311,22 @@ int tm_op4_rep_penalty(void* logits, int dtype, int64_t N, int64_t V, int64_t ro
  *   uniforms[c] < min(residual[t] / max(q_c[t], 1e-20), 1),  q_c = draft_probs[c],
  * and otherwise residual = max(residual - q_c, 0) / max(sum, 1e-20).  Depth is
  * unbounded (at most N accepted nodes).  When every child is rejected (or at a
- * leaf) the bonus token is the smallest j with residual[0] + .. + residual[j] >
- * bonus_u[0] * sum (inverse CDF; the reference calls torch.multinomial).
- * draft_probs: [N, V] fp32, row stride q_stride.  Children in CSR form with
- * num_edges entries, as in tm_op4_argmax_walk.  uniforms [N], bonus_u [1]
- * fp32 on the device.  residual: V fp32 of device memory (the final residual
- * on return).  V <= 2^25.  Outputs as tm_op4_argmax_walk.
+ * leaf) the bonus token is the first j maximising residual[j] / bonus_exp[j]
+ * (IEEE fp32 division): the reference's torch.multinomial(residual, 1,
+ * generator) draws exactly that index when bonus_exp is
+ * torch.empty(V).exponential_(1, generator) taken after the N uniforms, so
+ * the same generator state gives the reference's bonus (PyTorch samples one
+ * index by this exponential race).  draft_probs: [N, V] fp32, row stride
+ * q_stride.  Children in CSR form with num_edges entries, as in
+ * tm_op4_argmax_walk.  uniforms [N], bonus_exp [V] (> 0) fp32 on the device.
+ * residual: V fp32 of device memory (the final residual on return).
+ * V <= 2^25.  Outputs as tm_op4_argmax_walk.
  */
 int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int64_t V, int64_t row_stride,
                        const float* draft_probs, int64_t q_stride, const int64_t* tokens,
                        const int32_t* child_start, const int32_t* child_count,
                        const int32_t* child_list, int64_t num_edges, const float* uniforms,
-                       const float* bonus_u, float temperature, float* residual,
+                       const float* bonus_exp, float temperature, float* residual,
                        int64_t* accepted_slots,
                        int64_t* accepted_tokens, int64_t* result, void* stream);
 

@@ -1,8 +1,12 @@
 """TEST INFRASTRUCTURE ONLY: restatement of the op4 reference.
 
 * ``tree_verify``  treemoe/ref/verify_ref.py:35-103 (greedy branch exactly;
-  sampling branch with injected uniforms, temperature > 0).  Depth is
-  unbounded, as in the reference.
+  sampling branch with the generator's draws on the logits' device, or with
+  injected uniforms and bonus exponentials).  Depth is unbounded, as in the
+  reference.
+* ``exp_race``     torch.multinomial(p, 1, generator)'s one-sample draw
+  (argmax of p / e, e = empty_like(p).exponential_(1, generator)), which
+  the bonus of the sampling branch (verify_ref.py:87) is.
 * ``commit_tree``  treemoe/model/kv_cache.py:88-106 generalised to a page size
   P: tree slot s lives in scratch page ``scratch_pages[s // P]`` at offset
   ``s % P``; sequence position q lives in ``block_table[q // P]`` at ``q % P``.
@@ -17,16 +21,17 @@ def tree_verify(target_logits: torch.Tensor, draft_probs: torch.Tensor,
                 tree_tokens: torch.Tensor, children: list[list[int]],
                 temperature: float = 0.0, uniforms: torch.Tensor | None = None,
                 generator: torch.Generator | None = None,
-                bonus_uniform: float | None = None, return_residual: bool = False):
+                bonus_exp: torch.Tensor | None = None, return_residual: bool = False):
     """Returns (accepted_slots [N], accepted_tokens [N], bonus, num_accepted)
-    (+ the final residual when return_residual).  With bonus_uniform the
-    sampling-mode bonus is the inverse-CDF draw ``inverse_cdf(residual, u)``
-    instead of torch.multinomial."""
+    (+ the final residual when return_residual).  Without injected uniforms
+    the draws come from ``generator`` on the logits' device in the
+    reference's order (rand(N), then multinomial's exponentials); with
+    bonus_exp the sampling-mode bonus is ``exp_race(residual, bonus_exp)``."""
     n = target_logits.shape[0]
     slots: list[int] = []
     toks: list[int] = []
     if temperature != 0.0 and uniforms is None:
-        uniforms = torch.rand(n, generator=generator)
+        uniforms = torch.rand(n, generator=generator, device=target_logits.device)
     node = 0
     while True:
         if temperature == 0.0:
@@ -52,8 +57,8 @@ def tree_verify(target_logits: torch.Tensor, draft_probs: torch.Tensor,
         if taken < 0:
             if temperature == 0.0:
                 bonus = best
-            elif bonus_uniform is not None:
-                bonus = inverse_cdf(residual, bonus_uniform)
+            elif bonus_exp is not None:
+                bonus = exp_race(residual, bonus_exp)
             else:
                 bonus = int(torch.multinomial(residual, 1, generator=generator))
             break
@@ -70,17 +75,11 @@ def tree_verify(target_logits: torch.Tensor, draft_probs: torch.Tensor,
     return acc_slots, acc_toks, bonus, len(slots)
 
 
-def inverse_cdf(probs: torch.Tensor, u: float) -> int:
-    """Smallest j with probs[0] + .. + probs[j] > u * sum(probs), in float64
-    (the last positive entry when rounding leaves no such j)."""
-    p = probs.double()
-    c = torch.cumsum(p, 0)
-    target = u * float(c[-1])
-    idx = int(torch.searchsorted(c, torch.tensor([target], dtype=torch.float64), right=True))
-    if idx >= p.numel():
-        nz = (p > 0).nonzero().flatten()
-        idx = int(nz[-1]) if nz.numel() else 0
-    return idx
+def exp_race(probs: torch.Tensor, e: torch.Tensor) -> int:
+    """First index of the largest probs[j] / e[j] in fp32 (IEEE division):
+    the index torch.multinomial(probs, 1, generator) returns when e is
+    empty_like(probs).exponential_(1, generator) from the same state."""
+    return int(torch.argmax(probs.float() / e.float()))
 
 
 def rep_penalty_inplace(logits: torch.Tensor, prev_tokens, penalty: float) -> None:

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared_functions():
         assert hasattr(lib, name), name
     assert set(_capi.SIGNATURES) <= set(declared_functions())
-    assert lib.tm_version() == 40100
+    assert lib.tm_version() == 50000
 
 
 def test_status_strings():

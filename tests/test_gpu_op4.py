@@ -327,7 +327,7 @@ def _dt(t):
     return _capi.TM_DTYPE_F32 if t.dtype == torch.float32 else _capi.TM_DTYPE_BF16
 
 
-def _direct_sample(logits, q, tokens, children, uniforms, bonus_u, temperature):
+def _direct_sample(logits, q, tokens, children, uniforms, bonus_exp, temperature):
     """tm_op4_sample_walk on device tensors; returns (slots, toks, result, residual)."""
     from treemoe_spec_amd import _capi
     from treemoe_spec_amd.kernels.op4_commit import _children_csr
@@ -342,7 +342,7 @@ def _direct_sample(logits, q, tokens, children, uniforms, bonus_u, temperature):
     p = _capi.ptr
     _capi.call("tm_op4_sample_walk", p(logits), _dt(logits), n, v, logits.stride(0), p(q),
                q.stride(0), p(tokens), p(csr), p(csr) + 4 * n, p(csr) + 8 * n, edges, p(uniforms),
-               p(bonus_u), float(temperature), p(residual), p(slots), p(toks), p(result),
+               p(bonus_exp), float(temperature), p(residual), p(slots), p(toks), p(result),
                _capi.stream_of(logits.device))
     torch.cuda.synchronize()
     return slots.cpu(), toks.cpu(), result.cpu(), residual.cpu()
@@ -360,7 +360,7 @@ def test_sampling_injected_uniforms_kat(dtype):
         logits[i, w] = 10.0
     logits = logits.to(dtype).cuda()
     q = torch.full((3, 32), 1.0 / 32, device="cuda")
-    bu = torch.full((1,), 0.5, device="cuda")
+    bu = torch.ones(32, device="cuda")
     slots, toks, result, _ = _direct_sample(logits, q, tokens, children,
                                             torch.zeros(3, device="cuda"), bu, 1.0)
     assert int(result[1]) == 2 and slots.tolist() == [1, 2, -1] and toks.tolist() == [7, 9, -1]
@@ -391,8 +391,12 @@ def _sampling_case(seed, n, v, follow):
     (9, 16, 100000, 1.0), (10, 6, 9000, 1.2), (11, 2100, 300, 1.0), (12, 2100, 40000, 0.8)])
 def test_sampling_matches_oracle(dtype, seed, n, v, temperature):
     """Accept path, next root and bonus bit-exact against the oracle with the
-    same uniforms; the final residual within rtol 1e-4 / atol 1e-6 (fp32
-    softmax and residual updates with a different exp and summation order).
+    same uniforms and exponentials; the final residual within rtol 1e-4 /
+    atol 1e-6 (fp32 softmax and residual updates with a different exp and
+    summation order).  The bonus is exactly the first index of the largest
+    residual / e over the kernel's own residual (IEEE fp32 division), and the
+    oracle's index unless the oracle's two largest ratios lie closer than that
+    residual tolerance.
     bf16 logits: the oracle gets them widened to fp32, as the kernel reads them.
     V up to 32768 runs the register-resident walk (8, 16 or 32 entries per
     thread), larger V the tiled walk over a global residual (32769: a one-entry
@@ -403,18 +407,21 @@ def test_sampling_matches_oracle(dtype, seed, n, v, temperature):
         g, children, tokens, logits, q = _sampling_case(seed * 10 + rep, n, v, 0.8)
         logits = logits.to(dtype)
         u = torch.rand(n, generator=g)
-        bu = float(torch.rand(1, generator=g))
+        e = torch.empty(v).exponential_(1.0, generator=g)
         slots, toks, result, residual = _direct_sample(
-            logits.cuda(), q.cuda(), tokens.cuda(), children, u.cuda(),
-            torch.tensor([bu], device="cuda"), temperature)
+            logits.cuda(), q.cuda(), tokens.cuda(), children, u.cuda(), e.cuda(), temperature)
         r_slots, r_toks, r_bonus, r_num, r_res = op4_ref.tree_verify(
             logits.float(), q, tokens, children, temperature=temperature, uniforms=u,
-            bonus_uniform=bu, return_residual=True)
+            bonus_exp=e, return_residual=True)
         assert int(result[1]) == r_num
         assert torch.equal(slots, r_slots) and torch.equal(toks, r_toks)
         assert int(result[2]) == (int(r_slots[r_num - 1]) if r_num else 0)
         torch.testing.assert_close(residual, r_res.float(), rtol=1e-4, atol=1e-6)
-        assert int(result[0]) == r_bonus
+        bonus = int(result[0])
+        assert bonus == int(torch.argmax(residual / e))
+        if bonus != r_bonus:
+            ratio = r_res.float() / e
+            assert float(ratio[bonus]) >= float(ratio.max()) * (1 - 3e-4), (bonus, r_bonus)
 
 
 def test_sampling_first_token_distribution():
@@ -433,7 +440,7 @@ def test_sampling_first_token_distribution():
         tokens[:, c] = torch.multinomial(q[c], trials, replacement=True, generator=g)
     tokens = tokens.cuda()
     u = torch.rand(trials, 4, generator=g).cuda()
-    bu = torch.rand(trials, generator=g).cuda()
+    e = torch.empty(trials, v).exponential_(1.0, generator=g).cuda()
     q = q.cuda()
     from treemoe_spec_amd import _capi
     from treemoe_spec_amd.kernels.op4_commit import _children_csr
@@ -447,7 +454,7 @@ def test_sampling_first_token_distribution():
     stream = _capi.stream_of(logits.device)
     for t in range(trials):
         _capi.call("tm_op4_sample_walk", P(logits), _dt(logits), 4, v, v, P(q), v,
-                   P(tokens[t]), P(csr), P(csr) + 16, P(csr) + 32, edges, P(u[t]), P(bu[t]),
+                   P(tokens[t]), P(csr), P(csr) + 16, P(csr) + 32, edges, P(u[t]), P(e[t]),
                    temperature, P(residual), P(slots[t]), P(toks[t]), P(result[t]), stream)
     torch.cuda.synchronize()
     num = result[:, 1].cpu()
@@ -459,9 +466,11 @@ def test_sampling_first_token_distribution():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_fused_sampling_draws_from_the_generator_and_commits(dtype):
-    """fused_verify_commit(temperature > 0) draws N accept uniforms then one
-    bonus uniform from the caller's generator on the logits' device; the
-    commit moves [root] + accepted path, bytes equal to the oracle."""
+    """fused_verify_commit(temperature > 0) takes its draws from the caller's
+    generator as the reference does (rand(N), then torch.multinomial): the
+    oracle run on the GPU with a generator in the same state, calling
+    torch.multinomial itself, gives the same path and bonus; the commit moves
+    [root] + accepted path, bytes equal to the oracle."""
     _say(f"fused sampling + commit {dtype}")
     op4 = _op4()
     n, v, seq_len, page = 64, 4096, 37, 16
@@ -474,18 +483,41 @@ def test_fused_sampling_draws_from_the_generator_and_commits(dtype):
                                   temperature=0.9, generator=gen)
     torch.cuda.synchronize()
     gen2 = torch.Generator(device="cuda").manual_seed(1234)
-    u = torch.rand(n, generator=gen2, device="cuda").cpu()
-    bu = float(torch.rand(1, generator=gen2, device="cuda"))
     r_slots, r_toks, r_bonus, r_num = op4_ref.tree_verify(
-        logits.float().cpu(), q, tokens, children, temperature=0.9, uniforms=u,
-        bonus_uniform=bu)
+        logits.float(), q.cuda(), tokens, children, temperature=0.9, generator=gen2)
     assert int(res.num_accepted) == r_num and int(res.bonus_token) == r_bonus
     assert torch.equal(res.accepted_slots.cpu(), r_slots)
     assert torch.equal(res.accepted_tokens.cpu(), r_toks)
+    assert torch.equal(gen.get_state(), gen2.get_state())
     assert kv.seq_len == seq_len + r_num + 1
     commit = torch.cat([torch.zeros(1, dtype=torch.long), r_slots])
     assert op4_ref.commit_tree(k0, v0, commit, kv.tree_pages, kv.block_table, seq_len) == r_num + 1
     assert torch.equal(kv.k.cpu(), k0) and torch.equal(kv.v.cpu(), v0)
+
+
+@pytest.mark.parametrize("n,v,follow", [(64, 32000, 0.9), (16, 100000, 0.6), (2100, 1000, 0.5),
+                                        (8, 7, 0.0)])
+def test_sampling_seed_exact_with_reference_draws(n, v, follow):
+    """Same generator seed, same tokens: fused_verify_commit against the
+    reference's algorithm (the oracle on the GPU drawing torch.rand(N) and
+    calling torch.multinomial(residual, 1, generator)) over 12 seeds each,
+    register walk (V <= 32768), tiled walk (V = 100000) and a tree walked from
+    global memory (N = 2100).  Equal unless two of the race's ratios lie within
+    the residual's fp32 rounding difference, which these seeds do not hit."""
+    _say(f"seed-exact sampling n={n} v={v}")
+    op4 = _op4()
+    for seed in range(12):
+        g, children, tokens, logits, q = _sampling_case(500 + seed, n, v, follow)
+        logits, q = logits.cuda(), q.cuda()
+        res = op4.fused_verify_commit(logits, q, tokens.cuda(), None, children, temperature=0.8,
+                                      generator=torch.Generator(device="cuda").manual_seed(seed))
+        r_slots, r_toks, r_bonus, r_num = op4_ref.tree_verify(
+            logits, q, tokens, children, temperature=0.8,
+            generator=torch.Generator(device="cuda").manual_seed(seed))
+        assert int(res.num_accepted) == r_num, seed
+        assert int(res.bonus_token) == r_bonus, seed
+        assert torch.equal(res.accepted_slots.cpu(), r_slots)
+        assert torch.equal(res.accepted_tokens.cpu(), r_toks)
 
 
 # ---------------------------------------------------------- rep penalty --
@@ -644,12 +676,11 @@ def test_padded_tree_sampling(seed, num_valid):
     logits = torch.randn(n, v, generator=g)
     q = torch.softmax(torch.randn(n, v, generator=g), -1)
     uniforms = torch.rand(n, generator=g) * 0.3
-    bonus_u = torch.rand(1, generator=g)
+    bonus_exp = torch.empty(v).exponential_(1.0, generator=g)
     slots, toks, result, _ = _direct_sample(logits.cuda(), q.cuda(), tokens.cuda(), children,
-                                            uniforms.cuda(), bonus_u.cuda(), 1.0)
+                                            uniforms.cuda(), bonus_exp.cuda(), 1.0)
     r_slots, r_toks, r_bonus, r_num = op4_ref.tree_verify(
-        logits, q, tokens, children, temperature=1.0, uniforms=uniforms,
-        bonus_uniform=float(bonus_u))
+        logits, q, tokens, children, temperature=1.0, uniforms=uniforms, bonus_exp=bonus_exp)
     assert int(result[1]) == r_num and int(result[0]) == r_bonus
     assert torch.equal(slots, r_slots) and torch.equal(toks, r_toks)
 

@@ -164,50 +164,79 @@ def test_kv_commit_c_equals_torch_restatement(page):
         assert (p, o) in rows
 
 
-# ---------------- sampling: inverse CDF, rep penalty, distribution ----------------
+# ---------------- sampling: exponential race, rep penalty, distribution ----------------
 
-def test_inverse_cdf_brute_force():
-    """Smallest j whose prefix sum exceeds u * total, by exact rational arithmetic."""
-    from fractions import Fraction
-
-    g = torch.Generator().manual_seed(11)
-    for trial in range(40):
-        v = int(torch.randint(1, 9, (1,), generator=g))
-        p = torch.rand(v, generator=g, dtype=torch.float64)
-        p[torch.rand(v, generator=g) < 0.3] = 0.0
+@pytest.mark.parametrize("seed", range(0, 240, 8))
+def test_exp_race_is_torch_multinomial(seed):
+    """exp_race over empty(V).exponential_(1, g) picks torch.multinomial(p, 1, g)'s
+    index from the same generator state and leaves the generator where
+    multinomial leaves it (so later draws stay aligned): sizes from 1 to 70000,
+    planted zeros, unnormalised rows, one-hot rows."""
+    meta = torch.Generator().manual_seed(seed)
+    for k in range(8):
+        v = int(torch.randint(1, 70000 if k % 4 == 0 else 300, (1,), generator=meta))
+        p = torch.rand(v, generator=meta) ** 3 * float(torch.rand(1, generator=meta) * 7 + 0.1)
+        p[torch.rand(v, generator=meta) < 0.4] = 0.0
+        if k == 5:
+            p.zero_()
+            p[int(torch.randint(0, v, (1,), generator=meta))] = 0.25
         if float(p.sum()) == 0.0:
-            p[v // 2] = 0.5
-        for u in torch.rand(25, generator=g, dtype=torch.float64).tolist() + [0.0]:
-            exact = [Fraction(x) for x in p.tolist()]
-            target = Fraction(u) * sum(exact)
-            run, want = Fraction(0), None
-            for j, x in enumerate(exact):
-                run += x
-                if run > target:
-                    want = j
-                    break
-            assert op4_ref.inverse_cdf(p, u) == want
-            assert p[want] > 0  # a zero-probability token is never drawn
+            p[v // 2] = 1.0
+        state = seed * 100 + k
+        g1 = torch.Generator().manual_seed(state)
+        want = int(torch.multinomial(p, 1, generator=g1))
+        g2 = torch.Generator().manual_seed(state)
+        e = torch.empty(v).exponential_(1.0, generator=g2)
+        got = op4_ref.exp_race(p, e)
+        assert got == want, (seed, k, v)
+        assert p[got] > 0  # a zero-probability token is never drawn
+        assert torch.equal(g1.get_state(), g2.get_state())
 
 
-def test_inverse_cdf_special_cases():
-    assert op4_ref.inverse_cdf(torch.tensor([0.0, 0.0, 1.0, 0.0]), 0.999) == 2
-    assert op4_ref.inverse_cdf(torch.tensor([0.0, 0.25, 0.75]), 0.0) == 1
-    # u at the very top: the last positive entry
-    assert op4_ref.inverse_cdf(torch.tensor([0.5, 0.5, 0.0]), 1.0) == 1
+def test_exp_race_special_cases():
+    e = torch.ones(6)
+    # equal ratios: the lower index wins (torch.argmax's first occurrence)
+    assert op4_ref.exp_race(torch.tensor([0.1, 0.0, 0.3, 0.0, 0.0, 0.3]), e) == 2
+    # the ratio, not the probability, decides
+    assert op4_ref.exp_race(torch.tensor([0.6, 0.4]), torch.tensor([3.0, 1.0])) == 1
+    # zero probabilities lose to any positive one however small e is
+    assert op4_ref.exp_race(torch.tensor([0.0, 1e-30, 0.0]), torch.tensor([1e-30, 50.0, 1e-30])) == 1
+    # an all-zero row (multinomial refuses it) gives index 0
+    assert op4_ref.exp_race(torch.zeros(4), torch.rand(4) + 0.5) == 0
 
 
-def test_inverse_cdf_distribution():
-    """Empirical frequencies of inverse_cdf(p, U) match p (6-sigma binomial)."""
+def test_exp_race_distribution():
+    """Empirical frequencies of exp_race(p, Exp(1)) match p (6-sigma binomial)."""
     g = torch.Generator().manual_seed(5)
     p = torch.tensor([0.05, 0.0, 0.4, 0.15, 0.3, 0.1])
     trials = 20000
-    u = torch.rand(trials, generator=g, dtype=torch.float64)
-    counts = np.bincount([op4_ref.inverse_cdf(p, x) for x in u.tolist()], minlength=6)
+    e = torch.empty(trials, 6).exponential_(1.0, generator=g)
+    counts = np.bincount([op4_ref.exp_race(p, e[t]) for t in range(trials)], minlength=6)
     expect = p.double().numpy() * trials
     sigma = np.sqrt(trials * p.double().numpy() * (1 - p.double().numpy())) + 1e-9
     assert counts[1] == 0
     assert np.all(np.abs(counts - expect) <= 6 * sigma)
+
+
+def test_tree_verify_sampling_uses_the_reference_draws():
+    """Without injected draws the oracle takes rand(N) then multinomial's
+    exponentials from the generator: injecting exactly those draws gives the
+    same result, and the bonus is torch.multinomial's (verify_ref.py:51, :87)."""
+    v, n = 500, 9
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(n, v, generator=g) * 2
+    q = torch.softmax(torch.randn(n, v, generator=g) * 2, -1)
+    tokens = torch.randint(0, v, (n,), generator=g)
+    children = [[1, 2], [3], [4, 5], [], [6], [7], [8], [], []]
+    for seed in range(40):
+        a = op4_ref.tree_verify(logits, q, tokens, children, temperature=0.9,
+                                generator=torch.Generator().manual_seed(seed))
+        g2 = torch.Generator().manual_seed(seed)
+        u = torch.rand(n, generator=g2)
+        e = torch.empty(v).exponential_(1.0, generator=g2)
+        b = op4_ref.tree_verify(logits, q, tokens, children, temperature=0.9, uniforms=u,
+                                bonus_exp=e)
+        assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and a[2:] == b[2:]
 
 
 def test_rep_penalty_closed_form_power_of_two():
@@ -271,10 +300,10 @@ def test_tree_sampling_preserves_target_distribution():
         for c in (1, 2, 3):
             tokens[c] = int(torch.multinomial(q[c], 1, generator=g))
         u = torch.rand(4, generator=g)
-        bu = float(torch.rand(1, generator=g, dtype=torch.float64))
+        e = torch.empty(v).exponential_(1.0, generator=g)
         _, toks, bonus, num = op4_ref.tree_verify(logits, q, tokens, children,
                                                   temperature=temperature, uniforms=u,
-                                                  bonus_uniform=bu)
+                                                  bonus_exp=e)
         counts[int(toks[0]) if num else bonus] += 1
     sigma = np.sqrt(trials * p * (1 - p))
     assert np.all(np.abs(counts - trials * p) <= 6 * sigma)

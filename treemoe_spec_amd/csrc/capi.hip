@@ -3,7 +3,7 @@
 
 #include "tm_common.h"
 
-extern "C" int tm_version(void) { return 40100; }
+extern "C" int tm_version(void) { return 50000; }
 
 extern "C" int tm_host_device_pointer(void* host, void** device) {
   if (host == nullptr || device == nullptr) return TM_ERR_ARG;

@@ -409,8 +409,11 @@ tm_rep_apply_kernel(void* __restrict__ logits, int64_t row_stride,
 // uniforms[c] < min(residual[t] / max(q_c[t], 1e-20), 1), q_c = draft_probs[c];
 // otherwise residual = max(residual - q_c, 0) / max(sum, 1e-20).  An accepted
 // child becomes the node; when every child is rejected (or at a leaf) the
-// bonus token is the inverse-CDF sample of the residual at bonus_u.  Every
-// reduction is in a fixed order, so the result is deterministic.
+// bonus token is torch.multinomial(residual, 1)'s draw for the same generator
+// state: PyTorch samples one index as argmax_j residual[j] / e[j] over
+// e = empty_like(residual).exponential_(1, generator) (first maximum), and the
+// caller passes that e.  Every reduction is in a fixed order, so the result
+// is deterministic.
 constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 
@@ -452,9 +455,8 @@ __device__ __forceinline__ float logit_at(const void* logits, int64_t at) {
 // a butterfly over the wave, then the 16 wave values in wave order.
 struct SampRegShared {
   float red[2][kSampWaves];  // alternating buffers: one barrier per reduction
-  float wsum[kSampWaves];
+  int ridx[2][kSampWaves];   // the argmax indices beside red
   int flag;
-  int pick;
 };
 
 // Trees up to kSampStage nodes are staged in LDS before the walk, together
@@ -582,84 +584,54 @@ __device__ __forceinline__ void store_range(float* dst, int lo, int V, bool vec,
   }
 }
 
-// Inclusive prefix sums of the threads' chunk sums in thread order, starting
-// from `base`: returns this thread's, sets `exc` to the previous thread's
-// (`base` for thread 0; the very value that thread returns) and `total` to
-// thread kSampThreads - 1's.  Also resets sh.pick for block_pick.
-__device__ __forceinline__ float block_scan(float csum, float base, float& exc, float& total,
-                                            SampRegShared& sh) {
+// Workgroup argmax of (v, idx) pairs: the largest v, and among equal v the
+// lowest idx (v >= 0 or -1 for "none").  Returns the winner to every thread.
+__device__ __forceinline__ int block_argmax(float v, int idx, SampRegShared& sh, int& phase) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  float inc = csum;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float t = __shfl_up(inc, off);
-    if (lane >= off) inc = inc + t;
-  }
-  if (lane == 63) sh.wsum[wave] = inc;
-  if (threadIdx.x == 0) sh.pick = INT_MAX;
-  __syncthreads();
-  float wbase = base, run = base;
-#pragma unroll
-  for (int w = 0; w < kSampWaves; ++w) {
-    if (w == wave) wbase = run;
-    run = run + sh.wsum[w];
-  }
-  total = run;
-  inc = wbase + inc;
-  exc = __shfl_up(inc, 1);
-  if (lane == 0) exc = wbase;
-  return inc;
-}
-
-// Inverse CDF within one block scan: the first thread whose inclusive sum
-// passes `target` walks its chunk x[0..R) (entries lo..) from `exc` and picks
-// the first entry whose running sum passes it (its last nonzero entry when
-// rounding leaves the target at the chunk's end).  Returns the pick to every
-// thread, -1 when no thread passes.
-template <int R>
-__device__ __forceinline__ int block_pick(const float (&x)[R], int lo, float inc, float exc,
-                                          float target, SampRegShared& sh) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t pass = __ballot(inc > target);
-  if (lane == 0 && pass != 0) atomicMin(&sh.pick, wave * 64 + __builtin_ctzll(pass));
-  __syncthreads();
-  if ((int)threadIdx.x == sh.pick) {
-    int pick = -1, last = -1;
-    float run = exc;
-#pragma unroll
-    for (int i = 0; i < R; ++i) {
-      run = run + x[i];
-      if (pick < 0 && run > target) pick = lo + i;
-      if (x[i] > 0.0f) last = lo + i;
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(idx, off);
+    if (ov > v || (ov == v && oi < idx)) {
+      v = ov;
+      idx = oi;
     }
-    sh.flag = pick >= 0 ? pick : last;
   }
-  if (threadIdx.x == 0 && sh.pick == INT_MAX) sh.flag = -1;
-  __syncthreads();
-  return sh.flag;
-}
-
-// Workgroup max of an int (one reduction slot, as block_reduce_fast).
-__device__ __forceinline__ int block_max_int(int v, SampRegShared& sh, int& phase) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off));
   float* buf = sh.red[phase];
+  int* ibuf = sh.ridx[phase];
   phase ^= 1;
-  if (lane == 0) buf[wave] = __int_as_float(v);
+  if (lane == 0) {
+    buf[wave] = v;
+    ibuf[wave] = idx;
+  }
   __syncthreads();
-  int r = __float_as_int(buf[0]);
+  float bv = buf[0];
+  int bi = ibuf[0];
 #pragma unroll
-  for (int w = 1; w < kSampWaves; ++w) r = max(r, __float_as_int(buf[w]));
-  return r;
+  for (int w = 1; w < kSampWaves; ++w)
+    if (buf[w] > bv || (buf[w] == bv && ibuf[w] < bi)) {
+      bv = buf[w];
+      bi = ibuf[w];
+    }
+  return bi;
 }
 
+// One thread's part of the exponential race over entries lo .. lo + R - 1
+// (x: residual entries, e: the exponentials; entries at or past V skipped):
+// the first of its largest x[i] / e[i] (IEEE division, as torch's div).
 template <int R>
-__device__ __forceinline__ int last_nonzero(const float (&x)[R], int lo, int last) {
+__device__ __forceinline__ void race_chunk(const float (&x)[R], const float (&e)[R], int lo,
+                                           int V, float& best, int& at) {
 #pragma unroll
-  for (int i = 0; i < R; ++i)
-    if (x[i] > 0.0f) last = lo + i;
-  return last;
+  for (int i = 0; i < R; ++i) {
+    if (lo + i < V) {
+      const float t = x[i] / e[i];
+      if (t > best) {
+        best = t;
+        at = lo + i;
+      }
+    }
+  }
 }
 
 template <int kDtype, int R>
@@ -670,8 +642,9 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
                           const int32_t* __restrict__ child_start,
                           const int32_t* __restrict__ child_count,
                           const int32_t* __restrict__ child_list, int num_edges,
-                          const float* __restrict__ uniforms, const float* __restrict__ bonus_u,
-                          float temperature, float* __restrict__ res, int vec_res,
+                          const float* __restrict__ uniforms,
+                          const float* __restrict__ bonus_exp, int vec_e, float temperature,
+                          float* __restrict__ res, int vec_res,
                           int64_t* __restrict__ accepted_slots,
                           int64_t* __restrict__ accepted_tokens, int64_t* __restrict__ result) {
   __shared__ SampRegShared sh;
@@ -767,15 +740,13 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
     break;
   }
 
-  // bonus: smallest j with r[0] + .. + r[j] > bonus_u * total
-  float csum = 0.0f;
-#pragma unroll
-  for (int i = 0; i < R; ++i) csum = csum + r[i];
-  float exc, total;
-  const float inc = block_scan(csum, 0.0f, exc, total, sh);
-  int bonus = block_pick<R>(r, lo, inc, exc, bonus_u[0] * total, sh);
-  if (bonus < 0)  // target at or past the total: the last nonzero entry
-    bonus = max(block_max_int(last_nonzero<R>(r, lo, -1), sh, phase), 0);
+  // bonus: the exponential race, argmax_j r[j] / e[j], first maximum
+  float e[R];
+  load_range<TM_DTYPE_F32, R>(bonus_exp, lo, V, vec_e != 0, 1.0f, e);
+  float best = -1.0f;
+  int at = INT_MAX;
+  race_chunk<R>(r, e, lo, V, best, at);
+  const int bonus = block_argmax(best, at, sh, phase);
   if (tid == 0) {
     result[0] = bonus;
     result[1] = count;
@@ -794,12 +765,11 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
 // [tile * kSampTile + t * kSampTR, + kSampTR) of every tile, so it issues a
 // tile's loads at once and only ever reads back residual entries it wrote
 // itself.  Sums accumulate over the thread's entries tile by tile, then as in
-// the register kernel.  The bonus scan finds the tile whose running total
-// (tile totals in tile order) passes the target, then scans that tile.
+// the register kernel; the bonus race runs over the tiles in order.
 constexpr int kSampTR = 32;
 constexpr int kSampTile = kSampThreads * kSampTR;
 constexpr int kSampRegMax = kSampTile;          // V up to this: the register kernel
-constexpr int kSampMaxTiles = 1024;             // tile totals kept in LDS
+constexpr int kSampMaxTiles = 1024;             // bounds V (2^25)
 constexpr int64_t kSampMaxV = (int64_t)kSampMaxTiles * kSampTile;
 
 template <int kDtype>
@@ -810,14 +780,14 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
                             const int32_t* __restrict__ child_start,
                             const int32_t* __restrict__ child_count,
                             const int32_t* __restrict__ child_list, int num_edges,
-                            const float* __restrict__ uniforms, const float* __restrict__ bonus_u,
-                            float temperature, float* __restrict__ res, int vec_res,
+                            const float* __restrict__ uniforms,
+                            const float* __restrict__ bonus_exp, int vec_e, float temperature,
+                            float* __restrict__ res, int vec_res,
                             int64_t* __restrict__ accepted_slots,
                             int64_t* __restrict__ accepted_tokens,
                             int64_t* __restrict__ result) {
   __shared__ SampRegShared sh;
   __shared__ SampTree tree;
-  __shared__ float s_tile[kSampMaxTiles];
   const int tid = threadIdx.x;
   const int tiles = (V + kSampTile - 1) / kSampTile;
   const bool vl = vec_logits != 0, vq = vec_q != 0, vr = vec_res != 0;
@@ -920,55 +890,18 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
     break;
   }
 
-  // bonus: tile totals in tile order, then the scan of the tile that passes
-  float total = 0.0f;
+  // bonus: the exponential race over the tiles in order, argmax_j
+  // res[j] / e[j], first maximum (each thread's entries in index order)
+  float best = -1.0f;
+  int at = INT_MAX;
   for (int tl = 0; tl < tiles; ++tl) {
-    float x[kSampTR];
-    load_range<TM_DTYPE_F32, kSampTR>(res, tl * kSampTile + tid * kSampTR, V, vr, 0.0f, x);
-    float csum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kSampTR; ++i) csum = csum + x[i];
-    const float t = block_reduce_fast(csum, false, sh, phase);
-    if (tid == 0) s_tile[tl] = t;
-    total = total + t;
-  }
-  __syncthreads();
-  const float target = bonus_u[0] * total;
-  float base = 0.0f;
-  int ct = -1;
-  for (int tl = 0; tl < tiles; ++tl) {
-    const float next = base + s_tile[tl];
-    if (next > target) {
-      ct = tl;
-      break;
-    }
-    base = next;
-  }
-  int bonus = -1;
-  if (ct >= 0) {
-    const int lo = ct * kSampTile + tid * kSampTR;
-    float x[kSampTR];
+    const int lo = tl * kSampTile + tid * kSampTR;
+    float x[kSampTR], e[kSampTR];
     load_range<TM_DTYPE_F32, kSampTR>(res, lo, V, vr, 0.0f, x);
-    float csum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kSampTR; ++i) csum = csum + x[i];
-    float exc, tile_end;
-    const float inc = block_scan(csum, base, exc, tile_end, sh);
-    bonus = block_pick<kSampTR>(x, lo, inc, exc, target, sh);
-    // rounding left the target past this tile's scan: its last nonzero entry
-    if (bonus < 0) bonus = block_max_int(last_nonzero<kSampTR>(x, lo, -1), sh, phase);
+    load_range<TM_DTYPE_F32, kSampTR>(bonus_exp, lo, V, vec_e != 0, 1.0f, e);
+    race_chunk<kSampTR>(x, e, lo, V, best, at);
   }
-  if (bonus < 0) {
-    // target at or past the total: the last nonzero entry
-    int last = -1;
-    for (int tl = 0; tl < tiles; ++tl) {
-      const int lo = tl * kSampTile + tid * kSampTR;
-      float x[kSampTR];
-      load_range<TM_DTYPE_F32, kSampTR>(res, lo, V, vr, 0.0f, x);
-      last = last_nonzero<kSampTR>(x, lo, last);
-    }
-    bonus = max(block_max_int(last, sh, phase), 0);
-  }
+  const int bonus = block_argmax(best, at, sh, phase);
   if (tid == 0) {
     result[0] = bonus;
     result[1] = count;
@@ -1052,17 +985,19 @@ template <int kDtype>
 void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, const float* q,
                         int64_t q_stride, const int64_t* tokens, const int32_t* child_start,
                         const int32_t* child_count, const int32_t* child_list, int num_edges,
-                        const float* uniforms, const float* bonus_u, float temperature,
+                        const float* uniforms, const float* bonus_exp, float temperature,
                         float* res, int64_t* accepted_slots, int64_t* accepted_tokens,
                         int64_t* result, hipStream_t stream) {
   const int64_t elem = kDtype == TM_DTYPE_F32 ? 4 : 2;
   const int vl = ((uintptr_t)logits % 16 == 0 && (row_stride * elem) % 16 == 0) ? 1 : 0;
   const int vq = ((uintptr_t)q % 16 == 0 && q_stride % 4 == 0) ? 1 : 0;
   const int vr = ((uintptr_t)res % 16 == 0) ? 1 : 0;
+  const int ve = ((uintptr_t)bonus_exp % 16 == 0) ? 1 : 0;
 #define TM_SAMPLE_REG(R)                                                                       \
   hipLaunchKernelGGL((tm_sample_walk_reg_kernel<kDtype, R>), dim3(1), dim3(kSampThreads), 0,   \
                      stream, logits, N, V, row_stride, vl, q, q_stride, vq, tokens,           \
-                     child_start, child_count, child_list, num_edges, uniforms, bonus_u, temperature, res, \
+                     child_start, child_count, child_list, num_edges, uniforms, bonus_exp, ve,    \
+                     temperature, res,                                                        \
                      vr, accepted_slots, accepted_tokens, result)
   if (V <= kSampThreads * 8) {
     TM_SAMPLE_REG(8);
@@ -1074,8 +1009,8 @@ void launch_sample_walk(const void* logits, int N, int V, int64_t row_stride, co
   } else {
     hipLaunchKernelGGL(tm_sample_walk_tiled_kernel<kDtype>, dim3(1), dim3(kSampThreads), 0,
                        stream, logits, N, V, row_stride, vl, q, q_stride, vq, tokens,
-                       child_start, child_count, child_list, num_edges, uniforms, bonus_u, temperature, res,
-                       vr, accepted_slots, accepted_tokens, result);
+                       child_start, child_count, child_list, num_edges, uniforms, bonus_exp, ve,
+                       temperature, res, vr, accepted_slots, accepted_tokens, result);
   }
 #undef TM_SAMPLE_REG
 }
@@ -1277,8 +1212,8 @@ extern "C" int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int6
                                   int64_t row_stride, const float* draft_probs, int64_t q_stride,
                                   const int64_t* tokens, const int32_t* child_start,
                                   const int32_t* child_count, const int32_t* child_list,
-                                  int64_t num_edges, const float* uniforms, const float* bonus_u,
-                                  float temperature, float* residual,
+                                  int64_t num_edges, const float* uniforms,
+                                  const float* bonus_exp, float temperature, float* residual,
                                   int64_t* accepted_slots, int64_t* accepted_tokens,
                                   int64_t* result, void* stream) {
   if (N < 1 || N > (1 << 20) || V < 1 || V > kSampMaxV || row_stride < V || q_stride < V ||
@@ -1289,12 +1224,12 @@ extern "C" int tm_op4_sample_walk(const void* logits, int dtype, int64_t N, int6
   if (dtype == TM_DTYPE_F32) {
     launch_sample_walk<TM_DTYPE_F32>(logits, (int)N, (int)V, row_stride, draft_probs, q_stride,
                                      tokens, child_start, child_count, child_list, (int)num_edges, uniforms,
-                                     bonus_u, temperature, residual, accepted_slots,
+                                     bonus_exp, temperature, residual, accepted_slots,
                                      accepted_tokens, result, (hipStream_t)stream);
   } else {
     launch_sample_walk<TM_DTYPE_BF16>(logits, (int)N, (int)V, row_stride, draft_probs, q_stride,
                                       tokens, child_start, child_count, child_list, (int)num_edges, uniforms,
-                                      bonus_u, temperature, residual, accepted_slots,
+                                      bonus_exp, temperature, residual, accepted_slots,
                                       accepted_tokens, result, (hipStream_t)stream);
   }
   TM_HIP_CHECK_LAUNCH();

@@ -22,10 +22,13 @@ probabilities tie and the lower index wins).
 Sampling (temperature > 0) follows the reference's routing of that mode to
 ``tree_verify_ref`` (:187-196): the walk is unbounded (max_depth and
 rep_penalty are not used), the accept draws are ``torch.rand(N, generator)``
-on the logits' device as in the reference, and the bonus token is an
-inverse-CDF draw of the residual at one more uniform from the same generator
-(the reference calls torch.multinomial: same distribution, different use of
-the random stream).  One launch, ``tm_op4_sample_walk``.
+on the logits' device as in the reference, and the bonus token is the
+reference's ``torch.multinomial(residual, 1, generator)`` draw: PyTorch
+samples one index as the argmax of residual / e over
+e = empty_like(residual).exponential_(1, generator), so the host draws that e
+from the same generator and the kernel runs the race.  One launch,
+``tm_op4_sample_walk``; no host synchronisation (the reference's multinomial
+checks its input on the host twice).
 """
 
 from __future__ import annotations
@@ -305,11 +308,14 @@ def fused_verify_commit(
             raise ValueError("sampling needs draft_probs [N, V] float32 on the logits' device "
                              "with unit stride along V")
         uniforms = torch.rand(n, generator=generator, device=dev)  # reference verify_ref.py:51
-        bonus_u = torch.rand(1, generator=generator, device=dev)
+        # torch.multinomial(residual, 1, generator) (reference :87) is
+        # argmax(residual / e) over these exponentials, drawn next
+        bonus_exp = torch.empty(v, dtype=torch.float32, device=dev).exponential_(
+            1.0, generator=generator)
         residual = torch.empty(v, dtype=torch.float32, device=dev)
         call("tm_op4_sample_walk", ptr(target_logits), dtype, n, v, target_logits.stride(0),
              ptr(q), q.stride(0), ptr(tokens), c_start, c_count, c_list, num_edges,
-             ptr(uniforms), ptr(bonus_u), float(temperature), ptr(residual), p_slots, p_toks,
+             ptr(uniforms), ptr(bonus_exp), float(temperature), ptr(residual), p_slots, p_toks,
              p_result, stream)
         commit_depth = _tree_depth(children)
     else:
