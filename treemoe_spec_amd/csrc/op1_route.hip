@@ -137,16 +137,19 @@ tm_router_rows_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict
   __shared__ uint4 s_w[kRowsLdsChunks];
   __shared__ float s_logit[kWaves][TM_MAX_EXPERTS];
   const int nchunk = H >> 3;  // = 64 XC
-  const uint4* wg4 = reinterpret_cast<const uint4*>(wg);
-  for (int i = threadIdx.x; i < E * nchunk; i += kThreads) s_w[i] = wg4[i];
-  tm_lds_barrier();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int t = blockIdx.x * kWaves + wave;
-  if (t >= T) return;
-  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)t * H);
+  // the token's row is requested before the W_g copy, so the two memory
+  // round trips overlap instead of following each other (T = 2048: 14.9 ->
+  // 14.2 us)
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)min(t, T - 1) * H);
   uint4 xv[XC];
 #pragma unroll
   for (int u = 0; u < XC; ++u) xv[u] = xr[lane + 64 * u];
+  const uint4* wg4 = reinterpret_cast<const uint4*>(wg);
+  for (int i = threadIdx.x; i < E * nchunk; i += kThreads) s_w[i] = wg4[i];
+  tm_lds_barrier();
+  if (t >= T) return;
   for (int e = 0; e < E; ++e) {
     const uint4* wr = s_w + e * nchunk;
     float acc = 0.0f;
