@@ -811,11 +811,15 @@ tm_prefill_gemm2_kernel(const uint16_t* __restrict__ h, const uint16_t* __restri
   __shared__ __attribute__((aligned(16))) uint8_t s2[C::STAGE];
   __shared__ __attribute__((aligned(16))) uint8_t s3[C::NSTAGE > 3 ? C::STAGE : 16];
   static_assert(C::NW == 8, "down GEMM: 8 waves, 64 output columns per column group");
-  int mt, job;  // job = (column block, segment)
-  const int ncol = (H / C::PBN) * nsplit;
+  int mt, job;  // job = (segment, column block), segment-major
+  const int ncb = H / C::PBN;
+  const int ncol = ncb * nsplit;
   if (!expert_job<C>((int)blockIdx.x, offsets, E, mt_max, ncol, &mt, &job)) return;
-  const int cb = job / nsplit;
-  const int seg = job - cb * nsplit;
+  // Each XCD owns a contiguous range of these jobs, so segment-major puts
+  // one K segment on each XCD (2 segments over 8 XCDs: 4 each) and an XCD
+  // reads the h rows of its segment only, instead of all of h.
+  const int seg = job / ncb;
+  const int cb = job - seg * ncb;
   int e, p0, rows;
   bool single;
   if (!find_mtile<C>(offsets, tiles, max_tiles, E, mt, &e, &p0, &rows, &single)) return;
