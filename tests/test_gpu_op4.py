@@ -668,6 +668,43 @@ def test_padded_tree_greedy(seed, num_valid):
     assert torch.equal(res.accepted_tokens.cpu(), ref[1])
 
 
+@pytest.mark.parametrize("v", [1000, 40000])
+@pytest.mark.parametrize("where", ["root", "deep", "draft"])
+def test_sampling_nan_follows_the_reference(where, v):
+    """NaN logits or draft rows: the accept test and the residual update keep
+    NaN as torch's clamps do, so every child at that node is rejected
+    (u < NaN is false) exactly as in the oracle, and the bonus is the first
+    NaN of the race (torch.argmax's order), an index inside the vocabulary.
+    Register walk (V = 1000) and tiled walk (V = 40000)."""
+    _say(f"sampling NaN {where} v={v}")
+    n = 12
+    g = torch.Generator().manual_seed(31)
+    children = [[1, 2], [3], [], [4, 5], [6], [], [7], [], [], [], [], []]
+    tokens = torch.randint(0, v, (n,), generator=g)
+    logits = torch.randn(n, v, generator=g) * 2
+    q = torch.softmax(torch.randn(n, v, generator=g), -1)
+    # plant acceptance of 1 -> 3 so that a deeper node is reached
+    for node, child in ((0, 1), (1, 3)):
+        logits[node, tokens[child]] = 30.0
+        q[child, tokens[child]] = 1e-6
+    if where == "root":
+        logits[0, 5] = float("nan")
+    elif where == "deep":
+        logits[3, 7] = float("nan")
+    else:
+        q[4] = float("nan")
+    u = torch.rand(n, generator=g) * 0.5
+    e = torch.empty(v).exponential_(1.0, generator=g)
+    slots, toks, result, _ = _direct_sample(logits.cuda(), q.cuda(), tokens.cuda(), children,
+                                            u.cuda(), e.cuda(), 1.0)
+    r_slots, r_toks, r_bonus, r_num = op4_ref.tree_verify(
+        logits, q, tokens, children, temperature=1.0, uniforms=u, bonus_exp=e)
+    assert int(result[1]) == r_num and int(result[0]) == r_bonus
+    assert torch.equal(slots, r_slots) and torch.equal(toks, r_toks)
+    assert 0 <= int(result[0]) < v
+    assert r_num == {"root": 0, "deep": 2, "draft": 2}[where]
+
+
 @pytest.mark.parametrize("seed,num_valid", [(4, 40), (5, 2)])
 def test_padded_tree_sampling(seed, num_valid):
     _say(f"padded tree sampling seed={seed} valid={num_valid}")

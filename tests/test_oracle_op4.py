@@ -203,6 +203,10 @@ def test_exp_race_special_cases():
     assert op4_ref.exp_race(torch.tensor([0.0, 1e-30, 0.0]), torch.tensor([1e-30, 50.0, 1e-30])) == 1
     # an all-zero row (multinomial refuses it) gives index 0
     assert op4_ref.exp_race(torch.zeros(4), torch.rand(4) + 0.5) == 0
+    # NaN ratios rank above every number, the first one wins (torch.argmax)
+    nan = float("nan")
+    assert op4_ref.exp_race(torch.tensor([0.1, nan, 0.3, nan]), torch.ones(4)) == 1
+    assert op4_ref.exp_race(torch.tensor([nan, nan]), torch.ones(2)) == 0
 
 
 def test_exp_race_distribution():

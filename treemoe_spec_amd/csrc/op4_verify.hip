@@ -417,6 +417,20 @@ tm_rep_apply_kernel(void* __restrict__ logits, int64_t row_stride,
 constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 
+// torch.clamp_min / clamp(max=) on one value: a NaN stays NaN (fmaxf and
+// fminf would return the bound), so NaN logits reject every child as in the
+// reference (u < NaN is false) instead of accepting the first.
+__device__ __forceinline__ float clamp_min_nan(float x, float lo) {
+  return x != x ? x : fmaxf(x, lo);
+}
+__device__ __forceinline__ float clamp_max_nan(float x, float hi) {
+  return x != x ? x : fminf(x, hi);
+}
+// e^d of a softmax entry with a NaN argument kept NaN (tm_expf_det returns 0
+// for it), so a NaN logit, a +inf one or a row of -inf makes the whole row
+// NaN as torch.softmax does.
+__device__ __forceinline__ float exp_nan(float d) { return d != d ? d : tm_expf_det(d); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off);
@@ -515,7 +529,7 @@ __device__ __forceinline__ int sample_accept(bool staged, const SampTree& s, int
                                              const float* __restrict__ q, int64_t q_stride) {
   const float u = staged ? s.u[c] : uniforms[c];
   const float qt = staged ? s.qtok[c] : q[(int64_t)c * q_stride + tok];
-  const float ratio = fminf(rv / fmaxf(qt, 1e-20f), 1.0f);
+  const float ratio = clamp_max_nan(rv / clamp_min_nan(qt, 1e-20f), 1.0f);
   return u < ratio ? 1 : 0;
 }
 
@@ -584,15 +598,24 @@ __device__ __forceinline__ void store_range(float* dst, int lo, int V, bool vec,
   }
 }
 
-// Workgroup argmax of (v, idx) pairs: the largest v, and among equal v the
-// lowest idx (v >= 0 or -1 for "none").  Returns the winner to every thread.
+// (v, i) precedes (w, j) in torch.argmax's order: NaN above every number,
+// then the larger value; among equal values (or two NaNs) the lower index.
+__device__ __forceinline__ bool argmax_before(float v, int i, float w, int j) {
+  const bool vn = v != v, wn = w != w;
+  if (vn != wn) return vn;
+  if (vn || v == w) return i < j;
+  return v > w;
+}
+
+// Workgroup argmax of (v, idx) pairs in argmax_before's order (v >= 0, NaN,
+// or -1 for "none").  Returns the winner to every thread.
 __device__ __forceinline__ int block_argmax(float v, int idx, SampRegShared& sh, int& phase) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(v, off);
     const int oi = __shfl_xor(idx, off);
-    if (ov > v || (ov == v && oi < idx)) {
+    if (argmax_before(ov, oi, v, idx)) {
       v = ov;
       idx = oi;
     }
@@ -609,7 +632,7 @@ __device__ __forceinline__ int block_argmax(float v, int idx, SampRegShared& sh,
   int bi = ibuf[0];
 #pragma unroll
   for (int w = 1; w < kSampWaves; ++w)
-    if (buf[w] > bv || (buf[w] == bv && ibuf[w] < bi)) {
+    if (argmax_before(buf[w], ibuf[w], bv, bi)) {
       bv = buf[w];
       bi = ibuf[w];
     }
@@ -618,7 +641,9 @@ __device__ __forceinline__ int block_argmax(float v, int idx, SampRegShared& sh,
 
 // One thread's part of the exponential race over entries lo .. lo + R - 1
 // (x: residual entries, e: the exponentials; entries at or past V skipped):
-// the first of its largest x[i] / e[i] (IEEE division, as torch's div).
+// the first of its largest x[i] / e[i] (IEEE division, as torch's div), a
+// NaN ratio counting as the largest, as torch.argmax does (a row of NaN
+// logits then yields index 0, never an index outside the vocabulary).
 template <int R>
 __device__ __forceinline__ void race_chunk(const float (&x)[R], const float (&e)[R], int lo,
                                            int V, float& best, int& at) {
@@ -626,7 +651,7 @@ __device__ __forceinline__ void race_chunk(const float (&x)[R], const float (&e)
   for (int i = 0; i < R; ++i) {
     if (lo + i < V) {
       const float t = x[i] / e[i];
-      if (t > best) {
+      if (t > best || (t != t && best == best)) {  // indices ascend: ties keep the first
         best = t;
         at = lo + i;
       }
@@ -675,7 +700,7 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      r[i] = tm_expf_det(r[i] - m);
+      r[i] = exp_nan(r[i] - m);
       s = s + r[i];
     }
     // the normalisations multiply by a reciprocal (within an ulp of dividing)
@@ -720,11 +745,11 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
                                       qc);
 #pragma unroll
         for (int i = 0; i < kQB; ++i) {
-          r[b + i] = fmaxf(r[b + i] - qc[i], 0.0f);
+          r[b + i] = clamp_min_nan(r[b + i] - qc[i], 0.0f);
           part = part + r[b + i];
         }
       }
-      const float rtot = 1.0f / fmaxf(block_reduce_fast(part, false, sh, phase), 1e-20f);
+      const float rtot = 1.0f / clamp_min_nan(block_reduce_fast(part, false, sh, phase), 1e-20f);
 #pragma unroll
       for (int i = 0; i < R; ++i) r[i] = r[i] * rtot;
     }
@@ -819,7 +844,7 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
       load_range<kDtype, kSampTR>(row, lo, V, vl, -INFINITY, x);
 #pragma unroll
       for (int i = 0; i < kSampTR; ++i) {
-        x[i] = tm_expf_det(div_by(x[i], temperature, rtemp) - m);
+        x[i] = exp_nan(div_by(x[i], temperature, rtemp) - m);
         s = s + x[i];
       }
       store_range<kSampTR>(res, lo, V, vr, x);
@@ -863,12 +888,12 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
         load_range<TM_DTYPE_F32, kSampTR>(qrow, lo, V, vq, 0.0f, qc);
 #pragma unroll
         for (int i = 0; i < kSampTR; ++i) {
-          x[i] = fmaxf(x[i] - qc[i], 0.0f);
+          x[i] = clamp_min_nan(x[i] - qc[i], 0.0f);
           part = part + x[i];
         }
         store_range<kSampTR>(res, lo, V, vr, x);
       }
-      const float rtot = 1.0f / fmaxf(block_reduce_fast(part, false, sh, phase), 1e-20f);
+      const float rtot = 1.0f / clamp_min_nan(block_reduce_fast(part, false, sh, phase), 1e-20f);
       for (int tl = 0; tl < tiles; ++tl) {
         const int lo = tl * kSampTile + tid * kSampTR;
         float x[kSampTR];
