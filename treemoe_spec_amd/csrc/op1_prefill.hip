@@ -342,17 +342,58 @@ __device__ __forceinline__ void compute_step(const uint8_t* st, const int (&brow
                                              f32x16_t (&acc)[M][2]) {
   const int lane = threadIdx.x & 63;
   const int wm = (threadIdx.x >> 6) & 1;
+  constexpr int S = C::PBK / 16;
+  if constexpr (S >= 4) {
+    // K steps of 64: the fragments of k-step s + 1 are read between the
+    // MFMAs of k-step s (one MFMA, then one LDS read, while reads remain), so
+    // each MFMA waits only for reads issued a k-step earlier.  Same MFMAs in
+    // the same order.  (Config 5 down GEMM 588 -> 569 us same-box; on the
+    // 256-row gate/up tile, whose steps have two k-steps, it measured slower,
+    // 1043 -> 1068 us, so that tile keeps the loop below.)
+    u32x4_t a[2][M], b[2][2];
 #pragma unroll
-  for (int s = 0; s < C::PBK / 16; ++s) {
-    u32x4_t a[M], b[2];
+    for (int i = 0; i < M; ++i) a[0][i] = frag<C>(st, 32 * M * wm + 32 * i, 0, lane);
 #pragma unroll
-    for (int i = 0; i < M; ++i) a[i] = frag<C>(st, 32 * M * wm + 32 * i, s, lane);
+    for (int j = 0; j < 2; ++j) b[0][j] = frag<C>(st + C::ABYTES, brow[j], 0, lane);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) b[j] = frag<C>(st + C::ABYTES, brow[j], s, lane);
+    for (int s = 0; s < S; ++s) {
+      const int cur = s & 1, nxt = cur ^ 1;
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < S) {
 #pragma unroll
-    for (int i = 0; i < M; ++i)
+        for (int i = 0; i < M; ++i) a[nxt][i] = frag<C>(st, 32 * M * wm + 32 * i, s + 1, lane);
 #pragma unroll
-      for (int j = 0; j < 2; ++j) acc[i][j] = pmfma<DT>(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j) b[nxt][j] = frag<C>(st + C::ABYTES, brow[j], s + 1, lane);
+      }
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = pmfma<DT>(a[cur][i], b[cur][j], acc[i][j]);
+      if (s + 1 < S) {
+#pragma unroll
+        for (int k = 0; k < M + 2 && k < 2 * M; ++k) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        }
+        if constexpr (2 * M > M + 2)
+          __builtin_amdgcn_sched_group_barrier(0x008, 2 * M - (M + 2), 0);
+      }
+    }
+    // keep the next step's wait, barrier and loads after these MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      u32x4_t a[M], b[2];
+#pragma unroll
+      for (int i = 0; i < M; ++i) a[i] = frag<C>(st, 32 * M * wm + 32 * i, s, lane);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) b[j] = frag<C>(st + C::ABYTES, brow[j], s, lane);
+#pragma unroll
+      for (int i = 0; i < M; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = pmfma<DT>(a[i], b[j], acc[i][j]);
+    }
   }
 }
 
