@@ -207,13 +207,17 @@ __device__ __forceinline__ void attend_stage(const AttnParams& p, const uint8_t*
   const uint8_t* vl = kl + kKBytes;
   // S^T = K Q^T over two 32-key tiles; lane holds keys
   // 32 kt + 8 (v/4) + 4 half + v%4 of query c32 in sc[kt][v]
+  // the two key tiles' chains alternate (k-step outer), so consecutive MFMAs
+  // do not wait on each other; each tile still sums its k-steps in order
   f32x16_t sc[2];
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
+  for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
     for (int v = 0; v < 16; ++v) sc[kt][v] = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < kHD / 16; ++ks) {
+  for (int ks = 0; ks < kHD / 16; ++ks) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
       const u32x4_t a = *reinterpret_cast<const u32x4_t*>(
           kl + (32 * kt + c32) * kKStride + ks * 32 + half * 16);
       sc[kt] = mfma32(a, qf[ks], sc[kt]);
