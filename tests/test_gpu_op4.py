@@ -671,11 +671,11 @@ def test_padded_tree_greedy(seed, num_valid):
 @pytest.mark.parametrize("v", [1000, 40000])
 @pytest.mark.parametrize("where", ["root", "deep", "draft"])
 def test_sampling_nan_follows_the_reference(where, v):
-    """NaN logits or draft rows: the accept test and the residual update keep
-    NaN as torch's clamps do, so every child at that node is rejected
-    (u < NaN is false) exactly as in the oracle, and the bonus is the first
-    NaN of the race (torch.argmax's order), an index inside the vocabulary.
-    Register walk (V = 1000) and tiled walk (V = 40000)."""
+    """NaN logits or draft rows: the softmax, the accept test and the
+    residual update keep NaN as torch does, so every child at that node is
+    rejected (u < NaN is false) exactly as in the oracle, and the bonus of the
+    all-NaN residual is torch.argmax's first NaN, index 0, inside the
+    vocabulary.  Register walk (V = 1000) and tiled walk (V = 40000)."""
     _say(f"sampling NaN {where} v={v}")
     n = 12
     g = torch.Generator().manual_seed(31)

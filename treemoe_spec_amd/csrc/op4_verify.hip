@@ -417,19 +417,23 @@ tm_rep_apply_kernel(void* __restrict__ logits, int64_t row_stride,
 constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / 64;
 
-// torch.clamp_min / clamp(max=) on one value: a NaN stays NaN (fmaxf and
+// NaN as torch has it.  torch.clamp_min / clamp(max=) keep a NaN (fmaxf and
 // fminf would return the bound), so NaN logits reject every child as in the
-// reference (u < NaN is false) instead of accepting the first.
+// reference (u < NaN is false) instead of accepting the first.  The softmax
+// maximum propagates NaN (IEEE maximum, one v_maximum3_f32 per two entries on
+// gfx950, no dearer than fmaxf): a NaN logit, a +inf one (inf - inf) or a
+// row of -inf makes every e^(x - m) 0 (tm_expf_det of NaN is 0), the sum 0
+// and the row 0 * (1 / 0) = NaN, as torch.softmax's.  (A NaN test on every
+// entry instead cost ~4 us per config-4 call: the walk is VALU-bound.)
 __device__ __forceinline__ float clamp_min_nan(float x, float lo) {
   return x != x ? x : fmaxf(x, lo);
 }
 __device__ __forceinline__ float clamp_max_nan(float x, float hi) {
   return x != x ? x : fminf(x, hi);
 }
-// e^d of a softmax entry with a NaN argument kept NaN (tm_expf_det returns 0
-// for it), so a NaN logit, a +inf one or a row of -inf makes the whole row
-// NaN as torch.softmax does.
-__device__ __forceinline__ float exp_nan(float d) { return d != d ? d : tm_expf_det(d); }
+__device__ __forceinline__ float max_nan(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -536,14 +540,19 @@ __device__ __forceinline__ int sample_accept(bool staged, const SampTree& s, int
 __device__ __forceinline__ float block_reduce_fast(float v, bool is_max, SampRegShared& sh,
                                                    int& phase) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  v = is_max ? wave_max(v) : wave_sum(v);
+  if (is_max) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = max_nan(v, __shfl_xor(v, off));
+  } else {
+    v = wave_sum(v);
+  }
   float* buf = sh.red[phase];
   phase ^= 1;
   if (lane == 0) buf[wave] = v;
   __syncthreads();
   float r = buf[0];
 #pragma unroll
-  for (int w = 1; w < kSampWaves; ++w) r = is_max ? fmaxf(r, buf[w]) : r + buf[w];
+  for (int w = 1; w < kSampWaves; ++w) r = is_max ? max_nan(r, buf[w]) : r + buf[w];
   return r;
 }
 
@@ -641,9 +650,13 @@ __device__ __forceinline__ int block_argmax(float v, int idx, SampRegShared& sh,
 
 // One thread's part of the exponential race over entries lo .. lo + R - 1
 // (x: residual entries, e: the exponentials; entries at or past V skipped):
-// the first of its largest x[i] / e[i] (IEEE division, as torch's div), a
-// NaN ratio counting as the largest, as torch.argmax does (a row of NaN
-// logits then yields index 0, never an index outside the vocabulary).
+// the first of its largest x[i] / e[i] (IEEE division, as torch's div).  A
+// NaN ratio never wins here; the residual is NaN-free or all NaN (a NaN logit
+// or draft entry reaches every entry through the softmax maximum or the
+// renormalising sum), and an all-NaN race finds nothing and is reported as
+// index 0, torch.argmax's first NaN (bonus_token).  Only an infinite draft
+// probability, not a probability, could leave a partly NaN residual, whose
+// NaN entries this race skips where torch.argmax would take the first.
 template <int R>
 __device__ __forceinline__ void race_chunk(const float (&x)[R], const float (&e)[R], int lo,
                                            int V, float& best, int& at) {
@@ -651,7 +664,7 @@ __device__ __forceinline__ void race_chunk(const float (&x)[R], const float (&e)
   for (int i = 0; i < R; ++i) {
     if (lo + i < V) {
       const float t = x[i] / e[i];
-      if (t > best || (t != t && best == best)) {  // indices ascend: ties keep the first
+      if (t > best) {  // indices ascend: ties keep the first
         best = t;
         at = lo + i;
       }
@@ -694,13 +707,13 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
 #pragma unroll
     for (int i = 0; i < R; ++i) {
       r[i] = div_by(r[i], temperature, rtemp);
-      m = fmaxf(m, r[i]);
+      m = max_nan(m, r[i]);
     }
     m = block_reduce_fast(m, true, sh, phase);
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      r[i] = exp_nan(r[i] - m);
+      r[i] = tm_expf_det(r[i] - m);
       s = s + r[i];
     }
     // the normalisations multiply by a reciprocal (within an ulp of dividing)
@@ -771,7 +784,8 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
   float best = -1.0f;
   int at = INT_MAX;
   race_chunk<R>(r, e, lo, V, best, at);
-  const int bonus = block_argmax(best, at, sh, phase);
+  const int won = block_argmax(best, at, sh, phase);
+  const int bonus = won == INT_MAX ? 0 : won;  // an all-NaN race: torch.argmax's index 0
   if (tid == 0) {
     result[0] = bonus;
     result[1] = count;
@@ -833,7 +847,7 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
       float x[kSampTR];
       load_range<kDtype, kSampTR>(row, tl * kSampTile + tid * kSampTR, V, vl, -INFINITY, x);
 #pragma unroll
-      for (int i = 0; i < kSampTR; ++i) m = fmaxf(m, div_by(x[i], temperature, rtemp));
+      for (int i = 0; i < kSampTR; ++i) m = max_nan(m, div_by(x[i], temperature, rtemp));
     }
     m = block_reduce_fast(m, true, sh, phase);
     // the exponentials go to res, then one pass scales them by 1 / sum
@@ -844,7 +858,7 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
       load_range<kDtype, kSampTR>(row, lo, V, vl, -INFINITY, x);
 #pragma unroll
       for (int i = 0; i < kSampTR; ++i) {
-        x[i] = exp_nan(div_by(x[i], temperature, rtemp) - m);
+        x[i] = tm_expf_det(div_by(x[i], temperature, rtemp) - m);
         s = s + x[i];
       }
       store_range<kSampTR>(res, lo, V, vr, x);
@@ -926,7 +940,8 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
     load_range<TM_DTYPE_F32, kSampTR>(bonus_exp, lo, V, vec_e != 0, 1.0f, e);
     race_chunk<kSampTR>(x, e, lo, V, best, at);
   }
-  const int bonus = block_argmax(best, at, sh, phase);
+  const int won = block_argmax(best, at, sh, phase);
+  const int bonus = won == INT_MAX ? 0 : won;  // an all-NaN race: torch.argmax's index 0
   if (tid == 0) {
     result[0] = bonus;
     result[1] = count;
