@@ -422,8 +422,7 @@ constexpr int kSampWaves = kSampThreads / 64;
 // reference (u < NaN is false) instead of accepting the first.  The softmax
 // maximum propagates NaN (IEEE maximum, one v_maximum3_f32 per two entries on
 // gfx950, no dearer than fmaxf): a NaN logit, a +inf one (inf - inf) or a
-// row of -inf makes every e^(x - m) 0 (tm_expf_det of NaN is 0), the sum 0
-// and the row 0 * (1 / 0) = NaN, as torch.softmax's.  (A NaN test on every
+// row of -inf makes the row NaN, as torch.softmax's.  (A NaN test on every
 // entry instead cost ~4 us per config-4 call: the walk is VALU-bound.)
 __device__ __forceinline__ float clamp_min_nan(float x, float lo) {
   return x != x ? x : fmaxf(x, lo);
@@ -433,6 +432,16 @@ __device__ __forceinline__ float clamp_max_nan(float x, float hi) {
 }
 __device__ __forceinline__ float max_nan(float a, float b) {
   return __builtin_elementwise_maximum(a, b);
+}
+// e^(x - m) for the sampling softmax, given ml = m log2(e): the hardware
+// exponential v_exp_f32 of fma(x, log2(e), -ml).  The walk is VALU-bound
+// (1024 threads over a vocabulary row per node) and the software tm_expf_det
+// costs ~15 operations per entry; the residual's parity with the reference is
+// a tolerance (torch.softmax rounds differently from either), so the cheaper
+// form serves.  NaN stays NaN (also inf - inf), -inf gives 0.
+constexpr float kLog2e = 1.44269504088896341f;
+__device__ __forceinline__ float exp_soft(float x, float ml) {
+  return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -ml));
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -695,6 +704,7 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
                q_stride);
   int phase = 0;
   const float rtemp = 1.0f / temperature;
+  const bool unit_t = temperature == 1.0f;
   int node = 0;
   int count = 0;
   float r[R];
@@ -704,16 +714,22 @@ tm_sample_walk_reg_kernel(const void* __restrict__ logits, int N, int V, int64_t
                       (int64_t)node * row_stride * (kDtype == TM_DTYPE_F32 ? 4 : 2);
     load_range<kDtype, R>(row, lo, V, vec_logits != 0, -INFINITY, r);
     float m = -INFINITY;
+    if (unit_t) {  // x / 1 = x: no division at temperature 1
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-      r[i] = div_by(r[i], temperature, rtemp);
-      m = max_nan(m, r[i]);
+      for (int i = 0; i < R; ++i) m = max_nan(m, r[i]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        r[i] = div_by(r[i], temperature, rtemp);
+        m = max_nan(m, r[i]);
+      }
     }
     m = block_reduce_fast(m, true, sh, phase);
+    const float ml = m * kLog2e;
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < R; ++i) {
-      r[i] = tm_expf_det(r[i] - m);
+      r[i] = exp_soft(r[i], ml);
       s = s + r[i];
     }
     // the normalisations multiply by a reciprocal (within an ulp of dividing)
@@ -835,6 +851,7 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
     stage_tree(tree, N, V, tokens, child_start, child_count, child_list, num_edges, uniforms, q,
                q_stride);
   const float rtemp = 1.0f / temperature;
+  const bool unit_t = temperature == 1.0f;
   int phase = 0;
   int node = 0;
   int count = 0;
@@ -847,19 +864,30 @@ tm_sample_walk_tiled_kernel(const void* __restrict__ logits, int N, int V, int64
       float x[kSampTR];
       load_range<kDtype, kSampTR>(row, tl * kSampTile + tid * kSampTR, V, vl, -INFINITY, x);
 #pragma unroll
-      for (int i = 0; i < kSampTR; ++i) m = max_nan(m, div_by(x[i], temperature, rtemp));
+      for (int i = 0; i < kSampTR; ++i) m = max_nan(m, x[i]);
     }
+    // max(x / T) = max(x) / T: correctly rounded division by T > 0 is monotone
     m = block_reduce_fast(m, true, sh, phase);
+    if (!unit_t) m = div_by(m, temperature, rtemp);
+    const float ml = m * kLog2e;
     // the exponentials go to res, then one pass scales them by 1 / sum
     float s = 0.0f;
     for (int tl = 0; tl < tiles; ++tl) {
       const int lo = tl * kSampTile + tid * kSampTR;
       float x[kSampTR];
       load_range<kDtype, kSampTR>(row, lo, V, vl, -INFINITY, x);
+      if (unit_t) {
 #pragma unroll
-      for (int i = 0; i < kSampTR; ++i) {
-        x[i] = tm_expf_det(div_by(x[i], temperature, rtemp) - m);
-        s = s + x[i];
+        for (int i = 0; i < kSampTR; ++i) {
+          x[i] = exp_soft(x[i], ml);
+          s = s + x[i];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < kSampTR; ++i) {
+          x[i] = exp_soft(div_by(x[i], temperature, rtemp), ml);
+          s = s + x[i];
+        }
       }
       store_range<kSampTR>(res, lo, V, vr, x);
     }
