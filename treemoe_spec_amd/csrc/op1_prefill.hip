@@ -24,7 +24,11 @@
 // uses the second when the experts average 384 rows or more and the third
 // when the tile list leaves at most 16 rows per entry.  A tile whose M-tile
 // holds fewer than BM real rows runs the MFMAs of the 64-row parts that hold
-// them only.
+// them only.  Where the MFMAs bound the kernel (the 256-row gate/up tile, and
+// the down GEMM when the experts average 384 rows or more) the two 4-wave
+// halves of a workgroup run the K loop half a step apart (k_loop_pp), so one
+// wave per SIMD issues MFMAs while the other reads its fragments (config 5,
+// same box: gate/up 1045 -> 990 us, down 576 -> 558 us, bit-identical).
 //
 // Gate/up: B = 128 rows of w1 and the same 128 rows of w3 (64 and 64 in the
 // 4-wave tile), so each wave holds the gate and up sums of the same outputs
@@ -53,8 +57,10 @@ constexpr uint32_t kOOR = 0x80000000u;   // out-of-range buffer offset: loads 0
 // Tile configuration: BM sorted rows per M-tile, K steps of BK, NS stages,
 // BN weight rows per workgroup, NTH threads (NTH / 64 waves as 2 row halves x
 // NTH / 128 column groups of 32 outputs, so BN = 32 x waves).
-template <int BM, int BK, int NS, int BN = 256, int NTH = 512>
+template <int BM, int BK, int NS, int BN = 256, int NTH = 512, bool PINGPONG = false>
 struct Tile {
+  // the two wave halves run the K loop half a step apart (k_loop_pp)
+  static constexpr bool PP = PINGPONG;
   static constexpr int PBM = BM;
   static constexpr int PBK = BK;
   static constexpr int NSTAGE = NS;
@@ -85,9 +91,12 @@ struct Tile {
   static_assert(NS == 3 || NS == 4, "stage rotation");
   static_assert(HROWS * HSTRIDE <= STAGE && (PBM + HROWS - 1) / HROWS <= NS, "h staging");
   static_assert(NS * STAGE <= 160 * 1024, "LDS");
+  static_assert(!PINGPONG || NTH == 512, "ping-pong: two halves of four waves");
 };
 using Tile128 = Tile<128, 64, 3>;
-using Tile256 = Tile<256, 32, 4>;
+using Tile256 = Tile<256, 32, 4, 256, 512, true>;
+// The down GEMM's tile where the experts average many rows (MFMA-bound).
+using Tile128PP = Tile<128, 64, 3, 256, 512, true>;
 // Few rows per expert: 64-row M-tiles against 128 weight rows with 4 waves,
 // 72 KB of LDS, so two workgroups share a CU.  Same per-output K order as
 // Tile128, so the same bits.
@@ -407,6 +416,108 @@ struct Stages {
   uint8_t* s3;
 };
 
+// A workgroup barrier (after this wave's LDS operations) that the compiler
+// schedules nothing across.
+__device__ __forceinline__ void pp_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  tm_lds_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// All fragments of one staged step (S = BK / 16 k-steps) into registers.
+template <class C, int M>
+__device__ __forceinline__ void read_step(const uint8_t* st, const int (&brow)[2],
+                                          u32x4_t (&a)[C::PBK / 16][M],
+                                          u32x4_t (&b)[C::PBK / 16][2]) {
+  const int lane = threadIdx.x & 63;
+  const int wm = (threadIdx.x >> 6) & 1;
+#pragma unroll
+  for (int s = 0; s < C::PBK / 16; ++s) {
+#pragma unroll
+    for (int i = 0; i < M; ++i) a[s][i] = frag<C>(st, 32 * M * wm + 32 * i, s, lane);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) b[s][j] = frag<C>(st + C::ABYTES, brow[j], s, lane);
+  }
+}
+
+// The MFMAs of one staged step from registers, in compute_step's order.
+template <class C, int M, int DT>
+__device__ __forceinline__ void mfma_step(const u32x4_t (&a)[C::PBK / 16][M],
+                                          const u32x4_t (&b)[C::PBK / 16][2],
+                                          f32x16_t (&acc)[M][2]) {
+#pragma unroll
+  for (int s = 0; s < C::PBK / 16; ++s)
+#pragma unroll
+    for (int i = 0; i < M; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = pmfma<DT>(a[s][i], b[s][j], acc[i][j]);
+}
+
+// Ping-pong K loop (8 waves).  Waves 0-3 (half 0, one per SIMD) and waves
+// 4-7 (half 1) alternate between a memory phase (issue the loads of a future
+// step, read all fragments of the current step into registers) and an MFMA
+// phase, half a step apart, so on every SIMD one wave's MFMAs run while the
+// other wave reads its fragments; in the plain loop both waves of a SIMD
+// leave each step's barrier together and wait for their first fragments
+// together.  Barriers b(0), b(1), ... separate the phases:
+//   half 0, step k:  b(2k)  [memory k]  b(2k+1)  [MFMA k, wait loads of k+1]
+//   half 1, step k:  b(2k+1) [memory k, wait loads of k+1]  b(2k+2)  [MFMA k]
+// Step k's loads are complete in every thread before b(2k), so both halves
+// read it after that barrier; both have read step k-1 before b(2k), so the
+// loads of step k+NS-1 go into its stage after it.  Each half issues every
+// step's loads once, so the wait counts are those of k_loop; half 1 starts
+// with two barriers and half 0 ends with two, so both pass the same number.
+// Same MFMAs in the same order per output as k_loop.
+template <class C, int M, int DT, bool NTB>
+__device__ __forceinline__ void k_loop_pp(const Stages& sb, const DmaLoad<C>& d, int nk,
+                                          const int (&brow)[2], f32x16_t (&acc)[M][2]) {
+  constexpr int NS = C::NSTAGE;
+  constexpr int S = C::PBK / 16;
+  constexpr int W = (NS - 2) * C::LDS_PER_STEP;
+  uint8_t* const st[4] = {sb.s0, sb.s1, sb.s2, sb.s3};
+  const bool half1 = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 8)) != 0;
+#pragma unroll
+  for (int u = 0; u < NS - 1; ++u) dma_step<C, NTB>(d, st[u], u, nk);
+  wait_vm<W>();
+  u32x4_t a[S][M], b[S][2];
+  if (!half1) {
+    for (int k = 0; k < nk; k += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        if (u == 0 || k + u < nk) {
+          pp_barrier();                                                  // b(2k)
+          dma_step<C, NTB>(d, st[(u + NS - 1) % NS], k + u + NS - 1, nk);
+          read_step<C, M>(st[u], brow, a, b);
+          pp_barrier();                                                  // b(2k+1)
+          mfma_step<C, M, DT>(a, b, acc);
+          wait_vm<W>();
+        }
+      }
+    }
+    pp_barrier();
+    pp_barrier();
+  } else {
+    pp_barrier();
+    pp_barrier();
+    for (int k = 0; k < nk; k += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        if (u == 0 || k + u < nk) {
+          dma_step<C, NTB>(d, st[(u + NS - 1) % NS], k + u + NS - 1, nk);
+          read_step<C, M>(st[u], brow, a, b);
+          wait_vm<W>();
+          pp_barrier();                                                  // b(2k+2)
+          mfma_step<C, M, DT>(a, b, acc);
+          pp_barrier();                                                  // b(2k+3)
+        }
+      }
+    }
+  }
+  // the last loads (zeros past the end) must land before the stages are reused
+  wait_vm<0>();
+  __syncthreads();
+}
+
 // The K loop shared by both GEMMs over nk steps.  At the top of step k, steps
 // k .. k+NS-2 are in flight; the thread waits for its loads of step k, the
 // barrier makes every thread's loads visible and frees the stage of step k-1,
@@ -416,6 +527,10 @@ struct Stages {
 template <class C, int M, int DT, bool NTB>
 __device__ __forceinline__ void k_loop(const Stages& sb, const DmaLoad<C>& d, int nk,
                                        const int (&brow)[2], f32x16_t (&acc)[M][2]) {
+  if constexpr (C::PP) {
+    k_loop_pp<C, M, DT, NTB>(sb, d, nk, brow, acc);
+    return;
+  }
   constexpr int NS = C::NSTAGE;
   uint8_t* const st[4] = {sb.s0, sb.s1, sb.s2, sb.s3};
 #pragma unroll
@@ -1049,6 +1164,29 @@ extern "C" int tm_op1_prefill_gemm1_routed(
   return TM_OK;
 }
 
+namespace {
+
+// The down launch with tile C.
+template <class C>
+int launch_gemm2(const void* h, const void* w2, float* y, const float* gates_flat,
+                 const int32_t* sorted_slots, const int32_t* expert_offsets,
+                 const int32_t* tiles, int64_t max_tiles, int64_t split, int64_t T, int64_t H,
+                 int64_t I, int64_t E, int dtype, hipStream_t stream) {
+  const int64_t klen = I / split;
+  const int64_t mt_max = std::min<int64_t>(max_tiles, mtile_bound<C>(2 * T, E));
+  const int64_t jobs = launch_jobs(mt_max, (H / C::PBN) * split);
+  if (jobs > INT32_MAX) return TM_ERR_SHAPE;
+  hipLaunchKernelGGL((dtype == TM_DTYPE_F16 ? tm_prefill_gemm2_kernel<C, TM_DTYPE_F16>
+                                            : tm_prefill_gemm2_kernel<C, TM_DTYPE_BF16>),
+                     dim3((unsigned)jobs), dim3(C::NT), 0, stream, (const uint16_t*)h,
+                     (const uint16_t*)w2, y, gates_flat, sorted_slots, expert_offsets, tiles,
+                     (int)max_tiles, (int)E, (int)(2 * T), (int)H, (int)I, (int)klen,
+                     (int)split, (int)mt_max, (uint32_t)(2 * T * I * 2));
+  return TM_OK;
+}
+
+}  // namespace
+
 extern "C" int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y,
                                     const float* gates_flat, const int32_t* sorted_slots,
                                     const int32_t* expert_offsets, const int32_t* tiles,
@@ -1063,16 +1201,16 @@ extern "C" int tm_op1_prefill_gemm2(const void* h, const void* w2, float* y,
   if (klen < C::PBK || (klen % C::PBK) != 0 || H < C::PBN || (H % C::PBN) != 0) return TM_ERR_SHAPE;
   if (H * I * 2 >= (int64_t)kOOR || 2 * T * I * 2 >= (int64_t)kOOR) return TM_ERR_SHAPE;
   if (!aligned16(h) || !aligned16(w2) || !aligned16(y)) return TM_ERR_ALIGN;
-  const int64_t mt_max = std::min<int64_t>(max_tiles, mtile_bound<C>(2 * T, E));
-  const int64_t jobs = launch_jobs(mt_max, (H / C::PBN) * split);
-  if (jobs > INT32_MAX) return TM_ERR_SHAPE;
-  hipLaunchKernelGGL((dtype == TM_DTYPE_F16 ? tm_prefill_gemm2_kernel<C, TM_DTYPE_F16>
-                                            : tm_prefill_gemm2_kernel<C, TM_DTYPE_BF16>),
-                     dim3((unsigned)jobs), dim3(C::NT), 0,
-                     (hipStream_t)stream, (const uint16_t*)h, (const uint16_t*)w2, y, gates_flat,
-                     sorted_slots, expert_offsets, tiles, (int)max_tiles, (int)E, (int)(2 * T),
-                     (int)H, (int)I, (int)klen, (int)split, (int)mt_max,
-                     (uint32_t)(2 * T * I * 2));
+  // where the experts average 384 rows or more (the gate/up rule for its
+  // 256-row tile) the MFMAs bound the kernel and the ping-pong loop runs
+  const bool big = 2 * T >= 384 * E;
+  const int rc = big ? launch_gemm2<Tile128PP>(h, w2, y, gates_flat, sorted_slots,
+                                               expert_offsets, tiles, max_tiles, split, T, H,
+                                               I, E, dtype, (hipStream_t)stream)
+                     : launch_gemm2<Tile128>(h, w2, y, gates_flat, sorted_slots, expert_offsets,
+                                             tiles, max_tiles, split, T, H, I, E, dtype,
+                                             (hipStream_t)stream);
+  if (rc) return rc;
   TM_HIP_CHECK_LAUNCH();
   return TM_OK;
 }
