@@ -185,46 +185,45 @@ __device__ __forceinline__ bool job_of(int L, int n_mt, int ncol, int* mt, int* 
 template <class C>
 __device__ __forceinline__ bool expert_job(int L, const int32_t* __restrict__ offsets, int E,
                                            int mt_max, int ncol, int* mt, int* col) {
-  __shared__ int s_mt, s_col;
+  // every wave computes the job itself (no LDS, no barrier)
   const int x = L % kXcds, l = L / kXcds;
   const int cpx = (ncol + kXcds - 1) / kXcds;
-  if (threadIdx.x < 64) {
-    const int lane = threadIdx.x;
-    int n = 0;
-    if (lane < E) {
-      const int cnt = offsets[lane + 1] - offsets[lane];
-      n = (cnt + C::PBM - 1) / C::PBM;
-    }
-    int incl = n;
+  const int lane = threadIdx.x & 63;
+  int n = 0;
+  if (lane < E) {
+    const int cnt = offsets[lane + 1] - offsets[lane];
+    n = (cnt + C::PBM - 1) / C::PBM;
+  }
+  int incl = n;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int t = __shfl_up(incl, o);
-      if (lane >= o) incl += t;
-    }
-    const int first = incl - n;  // M-tiles of the experts before this lane's
-    const int total = __shfl(incl, 63);
-    const int active = __popcll(__ballot(n > 0));
-    if (total < 2 * active) {
-      // Mostly one M-tile per expert: the super-block order, whose jobs
-      // resident together read different experts' weights.
-      if (lane == 0) {
-        int mt = -1, col = 0;
-        const bool ok = job_of(L, min(total, mt_max), ncol, &mt, &col);
-        s_mt = ok ? mt : -1;
-        s_col = col;
-      }
-    } else {
-      if (lane == 0) s_mt = -1;  // (LDS stores of one wave land in order)
-      if (n > 0 && l >= first * cpx && l < incl * cpx) {
-        const int j = l - first * cpx;
-        s_mt = first + j % n;
-        s_col = x * cpx + j / n;
-      }
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o);
+    if (lane >= o) incl += t;
+  }
+  const int first = incl - n;  // M-tiles of the experts before this lane's
+  const int total = __shfl(incl, 63);
+  const int active = __popcll(__ballot(n > 0));
+  int m = -1, c = 0;
+  if (total < 2 * active) {
+    // Mostly one M-tile per expert: the super-block order, whose jobs
+    // resident together read different experts' weights.
+    int jm = -1, jc = 0;
+    const bool ok = job_of(L, min(total, mt_max), ncol, &jm, &jc);
+    m = ok ? jm : -1;
+    c = jc;
+  } else {
+    // the expert (lane) whose column range of this XCD holds l
+    const bool mine = n > 0 && l >= first * cpx && l < incl * cpx;
+    const unsigned long long owner = __ballot(mine);
+    if (owner != 0ull) {
+      const int src = __ffsll((long long)owner) - 1;
+      const int j = l - first * cpx;
+      m = __shfl(first + (n > 0 ? j % n : 0), src);
+      c = __shfl(x * cpx + (n > 0 ? j / n : 0), src);
     }
   }
-  __syncthreads();
-  *mt = s_mt;
-  *col = s_col;
+  *mt = __builtin_amdgcn_readfirstlane(m);
+  *col = __builtin_amdgcn_readfirstlane(c);
   return *mt >= 0 && *mt < mt_max && *col < ncol;
 }
 
