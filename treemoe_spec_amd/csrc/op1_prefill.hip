@@ -466,7 +466,10 @@ __device__ __forceinline__ void mfma_step(const u32x4_t (&a)[C::PBK / 16][M],
 // loads of step k+NS-1 go into its stage after it.  Each half issues every
 // step's loads once, so the wait counts are those of k_loop; half 1 starts
 // with two barriers and half 0 ends with two, so both pass the same number.
-// Same MFMAs in the same order per output as k_loop.
+// Same MFMAs in the same order per output as k_loop.  (A workgroup's waves
+// go to the CU's four SIMDs in turn, so waves w and w + 4 share a SIMD; the
+// ordering argument above holds for any placement, only the overlap needs
+// it.)
 template <class C, int M, int DT, bool NTB>
 __device__ __forceinline__ void k_loop_pp(const Stages& sb, const DmaLoad<C>& d, int nk,
                                           const int (&brow)[2], f32x16_t (&acc)[M][2]) {
